@@ -1,0 +1,159 @@
+/*
+ * mimir_prefixlm.h -- C ABI of the MI355X (gfx950) prefix-LM attention library
+ * (libmimir_prefixlm.so).
+ *
+ * Prefix-LM attention over packed variable-length sequences: inside sequence s
+ * (tokens cu_seqlens[s] .. cu_seqlens[s+1]) with prefix length p = prefix_lens[s],
+ * local query i may attend local key j iff
+ *
+ *     j < kend(i),   kend(i) = max(p, i + 1)        (is_causal == 0)
+ *     j < i + 1                                    (is_causal != 0)
+ *
+ * i.e. bidirectional inside the prefix and causal after it
+ * (reference: src/mimir/model/flash_attention_prefixlm_dense.py:61-69 and the
+ * Metal predicate src/mimir/model/flash_attention_prefixlm_mps.py:43-51).
+ *
+ * Layout: q [T, Hq, D], k/v [T, Hkv, D], out [T, Hq, D]; every tensor has a
+ * unit stride on the last (head_dim) axis and arbitrary token / head strides
+ * given in ELEMENTS.  v may therefore be the strided split of a fused
+ * gate/q/k/v projection (reference: src/mimir/model/layers.py:183-184).
+ * lse is float32 [Hq, T] (natural log of the softmax denominator, scale
+ * included), the FlashAttention varlen convention used by
+ * src/mimir/model/flash_attention_prefixlm_v2.py:159-160.
+ * GQA: query head h reads kv head h / (Hq / Hkv)
+ * (reference: flash_attention_prefixlm_dense.py:10-16, repeat_interleave).
+ *
+ * Query rows >= total_seqlen and rows outside every sequence produce O = 0,
+ * lse = -inf and zero dQ (reference: flash_attention_prefixlm_dense.py:43,79-80;
+ * flash_attention_prefixlm_v2.py:143,224-226).
+ *
+ * All device pointers are plain HIP device addresses; `stream` is a hipStream_t
+ * (passed as void* so that this header needs no HIP include).  Every entry point
+ * only enqueues work on `stream` and never synchronises it.  Status 0 is success;
+ * on failure mimir_prefixlm_last_error() returns a thread-local message.
+ */
+#ifndef MIMIR_PREFIXLM_H
+#define MIMIR_PREFIXLM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MIMIR_PREFIXLM_ABI_VERSION 1
+
+/* Element types of q/k/v/out/dout/dq/dk/dv (lse and the workspace are float32). */
+enum MimirDType {
+  MIMIR_DTYPE_FLOAT32 = 0,
+  MIMIR_DTYPE_BFLOAT16 = 1
+};
+
+/* Status codes.  The Python binding maps them to the exception types the
+ * reference raises for the same conditions. */
+enum MimirStatus {
+  MIMIR_OK = 0,
+  MIMIR_ERR_INVALID_ARGUMENT = 1, /* ValueError  (dense.py:14,54-55; fa4.py:437,460,505) */
+  MIMIR_ERR_UNSUPPORTED_DTYPE = 2,/* TypeError   (mps.py:1390-1391) */
+  MIMIR_ERR_UNSUPPORTED_SHAPE = 3,/* ValueError: head_dim / size not supported by the kernels */
+  MIMIR_ERR_HIP = 4               /* RuntimeError: a HIP launch or runtime call failed */
+};
+
+typedef struct MimirPrefixLMFwdParams {
+  const void* q;              /* [T, Hq, D]  */
+  const void* k;              /* [T, Hkv, D] */
+  const void* v;              /* [T, Hkv, D] */
+  void* out;                  /* [T, Hq, D], written for every row 0..T-1 */
+  float* lse;                 /* [Hq, T] float32, may be NULL */
+  const int32_t* prefix_lens; /* device int32 [>= numseqs]     */
+  const int32_t* causal_lens; /* device int32 [>= numseqs]     (only read by mimir_prefixlm_check_metadata) */
+  const int32_t* cu_seqlens;  /* device int32 [>= numseqs + 1] */
+  int64_t q_stride_token, q_stride_head;
+  int64_t k_stride_token, k_stride_head;
+  int64_t v_stride_token, v_stride_head;
+  int64_t out_stride_token, out_stride_head;
+  int64_t lse_stride_head;    /* lse[h * lse_stride_head + t] */
+  int32_t total_tokens;       /* T = q.shape[0] */
+  int32_t num_q_heads;        /* Hq */
+  int32_t num_kv_heads;       /* Hkv, Hq % Hkv == 0 */
+  int32_t head_dim;           /* D */
+  int32_t numseqs;
+  int32_t total_seqlen;
+  int32_t max_seqlen_all;     /* upper bound of cu_seqlens[s+1] - cu_seqlens[s] */
+  int32_t is_causal;
+  int32_t dtype;              /* enum MimirDType */
+  float softmax_scale;        /* > 0; the reference uses 1/sqrt(D) */
+} MimirPrefixLMFwdParams;
+
+typedef struct MimirPrefixLMBwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;            /* forward output [T, Hq, D] */
+  const void* dout;           /* upstream gradient [T, Hq, D] */
+  const float* lse;           /* forward lse [Hq, T] */
+  void* dq;                   /* [T, Hq, D]  */
+  void* dk;                   /* [T, Hkv, D] */
+  void* dv;                   /* [T, Hkv, D] */
+  const int32_t* prefix_lens;
+  const int32_t* causal_lens;
+  const int32_t* cu_seqlens;
+  int64_t q_stride_token, q_stride_head;
+  int64_t k_stride_token, k_stride_head;
+  int64_t v_stride_token, v_stride_head;
+  int64_t out_stride_token, out_stride_head;
+  int64_t dout_stride_token, dout_stride_head;
+  int64_t dq_stride_token, dq_stride_head;
+  int64_t dk_stride_token, dk_stride_head;
+  int64_t dv_stride_token, dv_stride_head;
+  int64_t lse_stride_head;
+  int32_t total_tokens;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t numseqs;
+  int32_t total_seqlen;
+  int32_t max_seqlen_all;
+  int32_t is_causal;
+  int32_t dtype;
+  float softmax_scale;
+  void* workspace;            /* device memory, >= mimir_prefixlm_bwd_workspace_bytes() */
+  size_t workspace_bytes;
+} MimirPrefixLMBwdParams;
+
+/* Forward: out (and lse if non-NULL).
+ * Replaces the FA4 two-pass forward, src/mimir/model/flash_attention_prefixlm_fa4.py:353-406
+ * (+ _fa4_varlen, fa4.py:17-50), the FA3 forward custom op
+ * src/mimir/model/flash_attention_prefixlm_v2.py:101-144, and the masked-SDPA loop
+ * src/mimir/model/flash_attention_prefixlm_dense.py:19-81. */
+int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* params, void* stream);
+
+/* Backward: dq, dk, dv from dout, out and lse.  Deterministic and atomic-free.
+ * Replaces the FA3 backward custom op src/mimir/model/flash_attention_prefixlm_v2.py:165-227,
+ * FA4's backward reached through fa4.py:153-179,309-331, and the Metal split
+ * backward src/mimir/model/flash_attention_prefixlm_mps.py:1456-1561. */
+int mimir_prefixlm_bwd(const MimirPrefixLMBwdParams* params, void* stream);
+
+/* Bytes of device workspace the backward needs (float32 delta [Hq, T]). */
+size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads);
+
+/* Device-side metadata check: writes to *bad_seq (device int32) the first s in
+ * [0, numseqs) with prefix_lens[s] + causal_lens[s] != cu_seqlens[s+1] - cu_seqlens[s]
+ * or a negative length, or -1 if none.  The reference raises ValueError for this
+ * (src/mimir/model/flash_attention_prefixlm_dense.py:54-55).  Asynchronous. */
+int mimir_prefixlm_check_metadata(const int32_t* prefix_lens, const int32_t* causal_lens,
+                                  const int32_t* cu_seqlens, int32_t numseqs,
+                                  int32_t* bad_seq, void* stream);
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char* mimir_prefixlm_last_error(void);
+
+/* MIMIR_PREFIXLM_ABI_VERSION of the loaded library. */
+int mimir_prefixlm_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIMIR_PREFIXLM_H */

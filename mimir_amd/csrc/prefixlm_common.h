@@ -1,0 +1,147 @@
+// Shared device helpers and internal launcher declarations for the gfx950
+// prefix-LM attention kernels.  Everything here is CDNA4-specific: wave64,
+// bf16 MFMA 32x32x16, buffer resources with hardware range checking,
+// ds_read_b64_tr_b16 transposing LDS reads and v_permlane32_swap.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mimir_prefixlm.h"
+
+namespace mimir {
+
+typedef __bf16 bf16_t;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------------------
+// Mask algebra.  Inside one sequence with prefix p the reference mask
+// (flash_attention_prefixlm_dense.py:61-69) is
+//   allowed(i, j) = (i < p && j < p) || (i >= p && j <= i)
+// which is exactly j < kend(i) with kend(i) = max(p, i + 1).  is_causal drops the
+// prefix (dense.py:61-62), i.e. p = 0.  The column dual is
+// qstart(j) = (j < p) ? 0 : j  (flash_attention_prefixlm_mps.py:1147-1149).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int kend_of(int p, int i) { return i + 1 > p ? i + 1 : p; }
+__device__ __forceinline__ int qstart_of(int p, int j) { return j < p ? 0 : j; }
+
+// Per-sequence geometry shared by every kernel.
+struct SeqGeom {
+  int start;  // first packed token of the sequence
+  int n;      // keys (sequence length)
+  int nq;     // active query rows: rows >= total_seqlen produce zeros
+  int p;      // effective prefix length, clamped to [0, n]; 0 when is_causal
+};
+
+// Sequence bounds are clamped to the packed length T so that malformed metadata
+// can never address memory outside the [T, ...] tensors.
+__device__ __forceinline__ SeqGeom load_seq(const int32_t* __restrict__ cu_seqlens,
+                                            const int32_t* __restrict__ prefix_lens, int s,
+                                            int total_seqlen, int is_causal, int T) {
+  SeqGeom g;
+  int start = cu_seqlens[s];
+  int end = cu_seqlens[s + 1];
+  start = start < 0 ? 0 : (start > T ? T : start);
+  end = end < start ? start : (end > T ? T : end);
+  g.start = start;
+  g.n = end - start;
+  int nq = total_seqlen - g.start;
+  g.nq = nq < 0 ? 0 : (nq > g.n ? g.n : nq);
+  int p = is_causal ? 0 : prefix_lens[s];
+  g.p = p < 0 ? 0 : (p > g.n ? g.n : p);
+  return g;
+}
+
+// ---------------------------------------------------------------------------
+// Buffer resources.  The descriptor's num_records bounds every access: a load
+// whose byte offset falls outside returns zeros, which is how rows beyond the
+// end of a sequence are zero-filled without branches.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Pair (x[l % 32], x[l % 32 + 32]) on every lane via v_permlane32_swap, which
+// exchanges vdst of lanes 32..63 with vsrc of lanes 0..31.  The two results are
+// read through int temporaries: __builtin_bit_cast applied directly to the
+// elements of the returned pair yields the first element twice on this compiler.
+__device__ __forceinline__ void halves(float x, float& lo, float& hi) {
+  const int xi = __float_as_int(x);
+  auto r = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+  const int a = r[0], b = r[1];
+  lo = __int_as_float(a);
+  hi = __int_as_float(b);
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  float a, b;
+  halves(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  float a, b;
+  halves(x, a, b);
+  return a + b;
+}
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Transposing LDS read.  Within each group of 16 lanes, lane j supplies the
+// address of 4 consecutive bf16 (row j/4, columns 4*(j%4)..+3 of a 4x16 block);
+// lane i receives column i of that block (rows 0..3).
+__device__ __forceinline__ bf16x4 lds_read_tr16(const bf16_t* p) {
+  i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(bf16x4, r);
+}
+
+__device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ bf16x8 to_bf16x8(f32x8 v) { return __builtin_convertvector(v, bf16x8); }
+
+// 16-byte-chunk XOR swizzle of a row-major [rows][D] bf16 tile in LDS: chunk c of
+// row r lives at chunk (c ^ (r & 7)).  Keeps the 32x16 MFMA operand reads and the
+// 4-row transposing reads free of bank conflicts.
+template <int D>
+__device__ __forceinline__ int swz(int row, int col) {
+  // col in elements; returns element offset inside the tile
+  const int chunk = (col >> 3) ^ (row & 7);
+  return row * D + (chunk << 3) + (col & 7);
+}
+
+}  // namespace mimir
+
+// Internal launchers (implemented per kernel file, dispatched from prefixlm_capi.cpp).
+hipError_t mimir_launch_fwd_bf16(const MimirPrefixLMFwdParams& p, hipStream_t stream);
+hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, hipStream_t stream);
+hipError_t mimir_launch_fwd_f32(const MimirPrefixLMFwdParams& p, hipStream_t stream);
+hipError_t mimir_launch_bwd_f32(const MimirPrefixLMBwdParams& p, hipStream_t stream);
+hipError_t mimir_launch_fill_fwd_padding(const MimirPrefixLMFwdParams& p, hipStream_t stream);
+hipError_t mimir_launch_fill_bwd_padding(const MimirPrefixLMBwdParams& p, hipStream_t stream);
+hipError_t mimir_launch_check_metadata(const int32_t* prefix_lens, const int32_t* causal_lens,
+                                       const int32_t* cu_seqlens, int32_t numseqs, int32_t* bad_seq,
+                                       hipStream_t stream);
+bool mimir_bf16_head_dim_supported(int d);
+bool mimir_f32_head_dim_supported(int d);

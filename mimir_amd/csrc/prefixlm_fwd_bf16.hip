@@ -1,0 +1,281 @@
+// bf16 prefix-LM attention forward for gfx950 (MI355X).
+//
+// One workgroup = 4 waves = 128 query rows of one (sequence, query head); each
+// wave owns 32 rows.  The kernel computes S^T = K Q^T on v_mfma_f32_32x32x16_bf16
+// so that every lane holds one query column of the score tile: the softmax
+// max/sum over keys is a per-lane reduction plus one v_permlane32_swap, the
+// running max / sum / rescale factor are lane-local, and the probabilities
+// P^T leave the accumulator already in the B-operand layout of O^T += V^T P^T.
+// V^T fragments come straight from the row-major V tile through
+// ds_read_b64_tr_b16.  K/V tiles of 64 keys are staged in LDS (XOR-swizzled
+// 16-byte chunks); the next tile is prefetched into registers while the current
+// one is consumed.
+//
+// Tile classes follow the mask algebra j < kend(i) = max(p, i + 1): key tiles at
+// or beyond a wave's largest kend are skipped, tiles entirely below its smallest
+// kend run unmasked (the whole prefix block is dense), the rest are masked
+// element-wise.  Reference semantics: flash_attention_prefixlm_dense.py:19-81;
+// the Metal online-softmax forward flash_attention_prefixlm_mps.py:391-476 is the
+// scalar ancestor of this loop (same m / l / lse = m + log(l) bookkeeping).
+#include "prefixlm_common.h"
+
+namespace {
+using namespace mimir;
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kBlockM = kWaves * 32;
+constexpr int kBlockN = 64;
+
+struct FwdArgs {
+  const bf16_t* q;
+  const bf16_t* k;
+  const bf16_t* v;
+  bf16_t* o;
+  float* lse;
+  const int32_t* prefix_lens;
+  const int32_t* cu_seqlens;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_sh;
+  int T;             // packed length
+  int group;         // Hq / Hkv
+  int total_seqlen;
+  int is_causal;
+  int num_m_tiles;
+  float scale;       // softmax scale
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ uint32_t rows_bytes(int rows, int64_t stride, int d) {
+  // bytes covering rows [0, rows) of a [rows][stride] bf16 matrix whose rows hold d values
+  return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + d) * 2) : 0u;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) {
+  constexpr int DT = D / 32;   // 32-row d tiles of O^T
+  constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
+  constexpr int CPR = D / 8;   // 16-byte chunks per row
+  constexpr int LOADS = kBlockN * CPR / kThreads;  // 16-byte chunks per thread per tile
+  static_assert(LOADS * kThreads == kBlockN * CPR, "tile load split");
+
+  __shared__ __attribute__((aligned(16))) bf16_t sK[kBlockN * D];
+  __shared__ __attribute__((aligned(16))) bf16_t sV[kBlockN * D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int hi = lane >> 5;
+
+  const int h = blockIdx.x;
+  const int mtile = a.num_m_tiles - 1 - (int)blockIdx.y;  // longest key ranges first
+  const int s = blockIdx.z;
+  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const int m0 = mtile * kBlockM;
+  if (m0 >= g.nq) return;
+  const int hk = h / a.group;
+
+  const int wg_qend = min(m0 + kBlockM, g.nq);
+  const int wg_kend = max(g.p, wg_qend);
+  const int nkt = (wg_kend + kBlockN - 1) / kBlockN;
+
+  const int qa = m0 + wave * 32;
+  const bool wave_active = qa < g.nq;
+  const int w_kend_max = wave_active ? max(g.p, min(qa + 32, g.nq)) : 0;
+  const int w_kend_min = max(g.p, qa + 1);
+  const int qpos = qa + l32;
+  const int kend_lane = kend_of(g.p, qpos);
+
+  const bf16_t* qbase = a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh;
+  const bf16_t* kbase_p = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
+  const bf16_t* vbase_p = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qbase, rows_bytes(g.nq, a.q_st, D));
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase_p, rows_bytes(g.n, a.k_st, D));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase_p, rows_bytes(g.n, a.v_st, D));
+
+  // Q^T B-operand fragments: lane holds query qpos, d = 16*ks + 8*hi .. +7.
+  bf16x8 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const uint32_t off = (uint32_t)(((int64_t)qpos * a.q_st + 16 * ks + 8 * hi) * 2);
+    qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, off));
+  }
+
+  // Global -> register prefetch of one K/V tile.
+  i32x4 pk[LOADS], pv[LOADS];
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int idx = tid + i * kThreads;
+      const int row = idx / CPR;
+      const int c = idx % CPR;
+      const int key = kt * kBlockN + row;
+      pk[i] = buf_load16(rk, (uint32_t)(((int64_t)key * a.k_st + c * 8) * 2));
+      pv[i] = buf_load16(rv, (uint32_t)(((int64_t)key * a.v_st + c * 8) * 2));
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int idx = tid + i * kThreads;
+      const int row = idx / CPR;
+      const int c = idx % CPR;
+      *(i32x4*)&sK[swz<D>(row, c * 8)] = pk[i];
+      *(i32x4*)&sV[swz<D>(row, c * 8)] = pv[i];
+    }
+  };
+
+  f32x16 oacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  const float c2 = a.scale_log2;
+
+  // lane geometry of the transposing V reads
+  const int tj = lane & 15;
+  const int tg = lane >> 4;
+  const int t_hi = tg >> 1;
+  const int t_dh = tg & 1;
+
+  load_tile(0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    __syncthreads();
+    store_tile();
+    __syncthreads();
+    if (kt + 1 < nkt) load_tile(kt + 1);
+
+    const int kb = kt * kBlockN;
+    if (!wave_active || kb >= w_kend_max) continue;
+
+    // S^T = K Q^T for 64 keys: two 32-key sub-tiles.
+    f32x16 st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      st[mt] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 kf = *(const bf16x8*)&sK[swz<D>(32 * mt + l32, 16 * ks + 8 * hi)];
+        st[mt] = mfma32(kf, qf[ks], st[mt]);
+      }
+    }
+
+    if (kb + kBlockN > w_kend_min) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kpos = kb + 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
+          if (kpos >= kend_lane) st[mt][r] = -INFINITY;
+        }
+    }
+
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
+    mx = xor32_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run) != 0) {
+      const float alpha = fast_exp2((m_run - m_new) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+    }
+    m_run = m_new;
+    const float mb = m_new * c2;
+
+    float lsum = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = fast_exp2(__builtin_fmaf(st[mt][r], c2, -mb));
+        st[mt][r] = pr;
+        lsum += pr;
+      }
+    l_run += lsum;
+
+    // P^T B-operand fragments (16 keys each), key order matching the V^T reads.
+    bf16x8 pf[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int mt = kk >> 1, s8 = (kk & 1) * 8;
+      f32x8 t;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = st[mt][s8 + e];
+      pf[kk] = to_bf16x8(t);
+    }
+
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int col = 32 * dt + 16 * t_dh + 4 * (tj & 3);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int krow = 16 * kk + 4 * t_hi + (tj >> 2);
+        const bf16x4 v0 = lds_read_tr16(&sV[swz<D>(krow, col)]);
+        const bf16x4 v1 = lds_read_tr16(&sV[swz<D>(krow + 8, col)]);
+        oacc[dt] = mfma32(cat8(v0, v1), pf[kk], oacc[dt]);
+      }
+    }
+  }
+
+  if (!wave_active) return;
+  const float l_tot = xor32_sum(l_run);
+  const float inv = 1.f / l_tot;
+  if (qpos < g.nq) {
+    bf16_t* orow = a.o + (int64_t)(g.start + qpos) * a.o_st + (int64_t)h * a.o_sh;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        f32x4 t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = oacc[dt][4 * rg + e] * inv;
+        *(bf16x4*)&orow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
+      }
+    if (hi == 0 && a.lse != nullptr)
+      a.lse[(int64_t)h * a.lse_sh + g.start + qpos] = m_run * a.scale + fast_log2(l_tot) * kLn2;
+  }
+}
+
+template <int D>
+hipError_t launch(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
+  FwdArgs a;
+  a.q = (const bf16_t*)p.q;
+  a.k = (const bf16_t*)p.k;
+  a.v = (const bf16_t*)p.v;
+  a.o = (bf16_t*)p.out;
+  a.lse = p.lse;
+  a.prefix_lens = p.prefix_lens;
+  a.cu_seqlens = p.cu_seqlens;
+  a.q_st = p.q_stride_token; a.q_sh = p.q_stride_head;
+  a.k_st = p.k_stride_token; a.k_sh = p.k_stride_head;
+  a.v_st = p.v_stride_token; a.v_sh = p.v_stride_head;
+  a.o_st = p.out_stride_token; a.o_sh = p.out_stride_head;
+  a.lse_sh = p.lse_stride_head;
+  a.T = p.total_tokens;
+  a.group = p.num_q_heads / p.num_kv_heads;
+  a.total_seqlen = p.total_seqlen;
+  a.is_causal = p.is_causal;
+  a.num_m_tiles = (p.max_seqlen_all + kBlockM - 1) / kBlockM;
+  a.scale = p.softmax_scale;
+  a.scale_log2 = p.softmax_scale * kLog2e;
+  if (a.num_m_tiles == 0 || p.numseqs == 0) return hipSuccess;
+  dim3 grid(p.num_q_heads, a.num_m_tiles, p.numseqs);
+  hipLaunchKernelGGL(fwd_bf16_kernel<D>, grid, dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool mimir_bf16_head_dim_supported(int d) { return d == 64 || d == 128; }
+
+hipError_t mimir_launch_fwd_bf16(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
+  switch (p.head_dim) {
+    case 64: return launch<64>(p, stream);
+    case 128: return launch<128>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}

@@ -1,0 +1,351 @@
+"""Drop-in prefix-LM attention for MI355X (gfx950).
+
+:func:`flash_attn_varlen_prefixlm` keeps the exact call signature of the
+reference entry point (src/mimir/model/flash_attention_prefixlm_v2.py:286-306,
+same keyword set as flash_attention_prefixlm_dispatch.py:80-106), so the Mimir2
+``Attention.forward`` call (src/mimir/model/layers.py:223-232) reaches this
+backend unchanged.  The work is done by hand-written HIP kernels in
+``libmimir_prefixlm.so`` behind a C ABI (include/mimir_prefixlm.h); this module
+only validates arguments, allocates outputs with torch's caching allocator and
+enqueues the library calls on torch's current stream.  There is no CPU or
+PyTorch fallback: tensors that are not on a ROCm device, or a missing library,
+raise.
+
+Layers:
+
+* ``torch.ops.mimir_amd.prefixlm_fwd`` / ``prefixlm_bwd`` -- ``torch.library``
+  custom ops with fake (meta) implementations, the pattern of
+  flash_attention_prefixlm_v2.py:101-162,165-246, so ``torch.compile`` traces
+  through without a graph break.
+* :class:`PrefixLMAttention` -- the autograd function (v2.py:249-283); it saves
+  q, k, v, O and the logsumexp and calls the atomic-free backward.
+* :func:`prefixlm_attn_fwd` -- lower-level entry returning ``(O, lse)`` with
+  ``lse`` float32 ``[Hq, T]`` (FA varlen layout, v2.py:159-160).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _capi
+
+__all__ = [
+    "PrefixLMAttention",
+    "check_metadata",
+    "flash_attn_varlen_prefixlm",
+    "prefixlm_attn_bwd",
+    "prefixlm_attn_fwd",
+    "set_validate_metadata",
+]
+
+ROUTING_KEYS = (
+    "prefix_cu_seqlens",
+    "prefix_idx",
+    "causal_idx",
+    "active_key_idx",
+    "active_cu_seqlens_q",
+    "active_cu_seqlens_k",
+)
+
+_DTYPES = {torch.float32: _capi.DTYPE_FLOAT32, torch.bfloat16: _capi.DTYPE_BFLOAT16}
+_validate_metadata = os.environ.get("MIMIR_PREFIXLM_VALIDATE", "0") not in ("", "0")
+
+
+def set_validate_metadata(enabled: bool) -> None:
+    """Check ``prefix_lens + causal_lens == seq_len`` on every call.
+
+    The check runs on the device and needs one host synchronisation per call, so
+    it is off by default (the FA4 path of the reference does not check either);
+    the reference's dense path raises ``ValueError`` for a mismatch
+    (flash_attention_prefixlm_dense.py:54-55) and so does this one when enabled.
+    """
+    global _validate_metadata
+    _validate_metadata = bool(enabled)
+
+
+def _scalar(x) -> int:
+    return int(x.item()) if isinstance(x, Tensor) else int(x)
+
+
+def _check_device_tensor(name: str, t: Tensor) -> None:
+    if t.device.type != "cuda" or torch.version.hip is None:
+        raise RuntimeError(
+            f"mimir_amd prefix-LM attention runs on ROCm GPUs only; {name} is on {t.device} "
+            "(there is no CPU fallback in this backend)"
+        )
+
+
+def _kernel_layout(t: Tensor) -> Tensor:
+    """Unit stride on head_dim, 16-byte aligned rows; copies otherwise."""
+    vec = 16 // t.element_size()
+    if (
+        t.stride(-1) != 1
+        or t.stride(0) % vec
+        or t.stride(1) % vec
+        or t.data_ptr() % 16
+        or t.stride(0) < t.shape[-1]
+    ):
+        t = t.contiguous()
+    return t
+
+
+def _metadata(t: Tensor, device: torch.device, n: int, name: str) -> Tensor:
+    if t.dim() != 1 or t.shape[0] < n:
+        raise ValueError(f"{name} must be a 1-D tensor with at least {n} entries, got shape {tuple(t.shape)}")
+    if t.device != device or t.dtype != torch.int32 or not t.is_contiguous():
+        t = t.to(device=device, dtype=torch.int32).contiguous()
+    return t
+
+
+def _geometry(q: Tensor, k: Tensor, v: Tensor):
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("q, k and v must be [tokens, heads, head_dim]")
+    if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError(f"incompatible q/k/v shapes {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise TypeError(f"q, k and v must share one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    if q.dtype not in _DTYPES:
+        raise TypeError(f"prefix-LM attention supports float32 and bfloat16 tensors only, got {q.dtype}")
+    hq, hkv = q.shape[1], k.shape[1]
+    if hq % hkv != 0:
+        raise ValueError(f"Query heads {hq} must be divisible by key/value heads {hkv}.")
+    return q.shape[0], hq, hkv, q.shape[2]
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def check_metadata(prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor, numseqs) -> None:
+    """Raise ``ValueError`` like flash_attention_prefixlm_dense.py:54-55 for a bad sequence.
+
+    Runs the library's device-side check and synchronises once.
+    """
+    lib = _capi.load()
+    n = _scalar(numseqs)
+    device = cu_seqlens.device
+    _check_device_tensor("cu_seqlens", cu_seqlens)
+    pl = _metadata(prefix_lens, device, n, "prefix_lens")
+    cl = _metadata(causal_lens, device, n, "causal_lens")
+    cu = _metadata(cu_seqlens, device, n + 1, "cu_seqlens")
+    bad = torch.empty(1, dtype=torch.int32, device=device)
+    status = lib.mimir_prefixlm_check_metadata(pl.data_ptr(), cl.data_ptr(), cu.data_ptr(), n, bad.data_ptr(), _stream(device))
+    _capi.raise_for_status(lib, status)
+    s = int(bad.item())
+    if s >= 0:
+        p, c = int(pl[s].item()), int(cl[s].item())
+        length = int(cu[s + 1].item()) - int(cu[s].item())
+        raise ValueError(f"Bad PrefixLM lengths for sequence {s}: {p} + {c} != {length}")
+
+
+def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
+              softmax_scale):
+    lib = _capi.load()
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _check_device_tensor(name, t)
+    T, hq, hkv, d = _geometry(q, k, v)
+    n = _scalar(numseqs)
+    device = q.device
+    pl = _metadata(prefix_lens, device, n, "prefix_lens")
+    cl = _metadata(causal_lens, device, n, "causal_lens")
+    cu = _metadata(cu_seqlens, device, n + 1, "cu_seqlens")
+    if _validate_metadata:
+        check_metadata(pl, cl, cu, n)
+    q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
+    out = torch.empty((T, hq, d), dtype=q.dtype, device=device)
+    lse = torch.empty((hq, T), dtype=torch.float32, device=device)
+    p = _capi.FwdParams(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+        pl.data_ptr(), cl.data_ptr(), cu.data_ptr(),
+        q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        out.stride(0), out.stride(1), lse.stride(0),
+        T, hq, hkv, d, n, _scalar(total_seqlen), _scalar(max_seqlen_all), int(bool(is_causal)),
+        _DTYPES[q.dtype], float(softmax_scale),
+    )
+    _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), _stream(device)))
+    return out, lse
+
+
+def _bwd_impl(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+              max_seqlen_all, softmax_scale):
+    lib = _capi.load()
+    T, hq, hkv, d = _geometry(q, k, v)
+    n = _scalar(numseqs)
+    device = q.device
+    pl = _metadata(prefix_lens, device, n, "prefix_lens")
+    cl = _metadata(causal_lens, device, n, "causal_lens")
+    cu = _metadata(cu_seqlens, device, n + 1, "cu_seqlens")
+    if dout.dtype != q.dtype:
+        dout = dout.to(q.dtype)
+    q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
+    out, dout = _kernel_layout(out), _kernel_layout(dout)
+    lse = lse.contiguous()
+    dq = torch.empty((T, hq, d), dtype=q.dtype, device=device)
+    dk = torch.empty((T, hkv, d), dtype=q.dtype, device=device)
+    dv = torch.empty((T, hkv, d), dtype=q.dtype, device=device)
+    ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_bytes(T, hq))
+    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=device)
+    p = _capi.BwdParams(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(), lse.data_ptr(),
+        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+        pl.data_ptr(), cl.data_ptr(), cu.data_ptr(),
+        q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        out.stride(0), out.stride(1), dout.stride(0), dout.stride(1),
+        dq.stride(0), dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1),
+        lse.stride(0),
+        T, hq, hkv, d, n, _scalar(total_seqlen), _scalar(max_seqlen_all), int(bool(is_causal)),
+        _DTYPES[q.dtype], float(softmax_scale), ws.data_ptr(), ws_bytes,
+    )
+    _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd(ctypes.byref(p), _stream(device)))
+    return dq, dk, dv
+
+
+@torch.library.custom_op("mimir_amd::prefixlm_fwd", mutates_args=())
+def _prefixlm_fwd_op(
+    q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
+    prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+    total_seqlen: Tensor, numseqs: Tensor, max_seqlen_all: Tensor, softmax_scale: float,
+) -> tuple[Tensor, Tensor]:
+    return _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+                     max_seqlen_all, softmax_scale)
+
+
+@_prefixlm_fwd_op.register_fake
+def _(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
+      softmax_scale):
+    return torch.empty_like(q, memory_format=torch.contiguous_format), q.new_empty(
+        (q.shape[1], q.shape[0]), dtype=torch.float32)
+
+
+@torch.library.custom_op("mimir_amd::prefixlm_bwd", mutates_args=())
+def _prefixlm_bwd_op(
+    dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor, is_causal: bool,
+    prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+    total_seqlen: Tensor, numseqs: Tensor, max_seqlen_all: Tensor, softmax_scale: float,
+) -> tuple[Tensor, Tensor, Tensor]:
+    return _bwd_impl(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
+                     numseqs, max_seqlen_all, softmax_scale)
+
+
+@_prefixlm_bwd_op.register_fake
+def _(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+      max_seqlen_all, softmax_scale):
+    cf = torch.contiguous_format
+    return (torch.empty_like(q, memory_format=cf), torch.empty_like(k, memory_format=cf),
+            torch.empty_like(v, memory_format=cf))
+
+
+def _cpu_scalar(x) -> Tensor:
+    if isinstance(x, Tensor):
+        return x if x.device.type == "cpu" else x.cpu()
+    return torch.tensor(int(x), dtype=torch.int64)
+
+
+class PrefixLMAttention(torch.autograd.Function):
+    """Autograd function over the two custom ops (flash_attention_prefixlm_v2.py:249-283)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+                max_seqlen_all, softmax_scale):
+        out, lse = _prefixlm_fwd_op(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
+                                    numseqs, max_seqlen_all, softmax_scale)
+        ctx.save_for_backward(q, k, v, out, lse, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+                              max_seqlen_all)
+        ctx.mark_non_differentiable(lse)
+        ctx.is_causal = bool(is_causal)
+        ctx.softmax_scale = float(softmax_scale)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        (q, k, v, out, lse, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+         max_seqlen_all) = ctx.saved_tensors
+        if dout is None:
+            dout = torch.zeros_like(out)
+        dq, dk, dv = _prefixlm_bwd_op(dout, q, k, v, out, lse, ctx.is_causal, prefix_lens, causal_lens,
+                                      cu_seqlens, total_seqlen, numseqs, max_seqlen_all, ctx.softmax_scale)
+        return dq, dk, dv, None, None, None, None, None, None, None, None
+
+
+def prefixlm_attn_fwd(
+    q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
+    prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+    total_seqlen, numseqs, max_seqlen_all, softmax_scale: Optional[float] = None,
+) -> tuple[Tensor, Tensor]:
+    """Differentiable prefix-LM attention returning ``(O, lse)``.
+
+    ``lse`` is float32 ``[Hq, T]``: natural log of the softmax denominator with
+    the scale included; rows outside every sequence or at/after
+    ``total_seqlen`` hold ``-inf`` (and O holds 0).  The gradient flows through
+    O only (``lse`` is treated as a non-differentiable auxiliary output).
+    """
+    scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else float(softmax_scale)
+    return PrefixLMAttention.apply(q, k, v, bool(is_causal), prefix_lens, causal_lens, cu_seqlens,
+                                   _cpu_scalar(total_seqlen), _cpu_scalar(numseqs), _cpu_scalar(max_seqlen_all),
+                                   scale)
+
+
+def prefixlm_attn_bwd(
+    dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor, is_causal: bool,
+    prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+    total_seqlen, numseqs, max_seqlen_all, softmax_scale: Optional[float] = None,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Explicit backward: ``(dQ, dK, dV)`` from ``dO``, ``O`` and ``lse``."""
+    scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else float(softmax_scale)
+    return _prefixlm_bwd_op(dout, q, k, v, out, lse, bool(is_causal), prefix_lens, causal_lens, cu_seqlens,
+                            _cpu_scalar(total_seqlen), _cpu_scalar(numseqs), _cpu_scalar(max_seqlen_all), scale)
+
+
+def flash_attn_varlen_prefixlm(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    is_causal: bool,
+    prefix_lens: Tensor,
+    causal_lens: Tensor,
+    cu_seqlens: Tensor,
+    total_seqlen: Tensor,
+    numseqs: Tensor,
+    max_seqlen_prefix: Tensor,
+    max_seqlen_causal: Tensor,
+    max_seqlen_all: Tensor,
+    *,
+    prefix_cu_seqlens: Optional[Tensor] = None,
+    prefix_idx: Optional[Tensor] = None,
+    causal_idx: Optional[Tensor] = None,
+    active_key_idx: Optional[Tensor] = None,
+    active_cu_seqlens_q: Optional[Tensor] = None,
+    active_cu_seqlens_k: Optional[Tensor] = None,
+    cu_seqlens_shifted: Optional[Tensor] = None,
+    prefix_mask: Optional[Tensor] = None,
+    causal_mask: Optional[Tensor] = None,
+    fa4_impl: str = "seqused",
+    fa4_grad_mask_impl: str = "triton",
+    fa4_output_combine_impl: str = "triton",
+) -> Tensor:
+    """Prefix-LM attention over packed sequences; returns O shaped like ``q``.
+
+    Signature of src/mimir/model/flash_attention_prefixlm_v2.py:286-306.  One
+    single-pass kernel covers both the bidirectional prefix block and the causal
+    suffix, so the two-pass routing tensors (``prefix_idx`` ... ``causal_mask``)
+    and the ``fa4_*`` knobs are accepted and ignored -- except that a partial set
+    of the six routing tensors raises ``ValueError`` as the reference's gather
+    backends do (flash_attention_prefixlm_rocm.py:71-72, fa4.py:505).
+    ``max_seqlen_prefix`` / ``max_seqlen_causal`` are not needed by the kernels.
+    """
+    routing = (prefix_cu_seqlens, prefix_idx, causal_idx, active_key_idx, active_cu_seqlens_q, active_cu_seqlens_k)
+    if any(r is None for r in routing) and not all(r is None for r in routing):
+        raise ValueError(f"PrefixLM routing tensors must provide all of {ROUTING_KEYS}")
+    out, _ = prefixlm_attn_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+                               max_seqlen_all)
+    return out
