@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Prefix-LM attention forward+backward throughput on one MI355X.
+
+One step = one forward and one backward pass of the prefix-LM attention
+operator over one packed batch, with every input already resident in HBM:
+``mimir_prefixlm_fwd`` followed by the backward stages (delta, dK/dV, dQ,
+padding fill) of ``mimir_prefixlm_bwd_stages``, all through the C ABI on
+torch's current stream.  The default workload is 8 sequences x 2048 tokens,
+16 q-heads / 4 kv-heads (GQA), head_dim 128, bf16, prefix lengths ~ U{0..2048}
+(seed 0).
+
+``value`` counts only attended (unmasked) pairs: fwd 4*D*Hq*N, bwd 10*D*Hq*N
+FLOPs with N = sum over sequences of (n^2 + n + p^2 - p)/2.  The roofline entry
+is for the kernel that takes the most time; its algorithmic FLOPs per launch are
+fwd 4*D*Hq*N, dK/dV 8*D*Hq*N (S recompute, dP, dV, dK) and dQ 2*D*Hq*N (dQ only;
+its S/dP recompute is not counted), so the three add up to the step's 14*D*Hq*N.
+Kernel durations come from HIP events recorded on the launch stream between the
+stages.  The CPU baseline times the oracle's restatement of the reference
+masked-SDPA path (fp32, autograd) on one sequence of the same batch.
+
+Prints exactly one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk, dense
+PEAK_F32_TFLOPS = 157.3     # fp32 matrix
+HBM_GBS = 8000.0
+METRIC = "prefix-LM attn fwd+bwd TFLOP/s (unmasked) bf16, % of MI355X MFMA peak"
+
+
+def _cores() -> int:
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_baseline(case, seconds_cap: float = 30.0) -> dict:
+    """Oracle masked-SDPA fwd+bwd (fp32) on the first sequence of the batch."""
+    import torch
+
+    from oracle.prefixlm_oracle import dense_forward_autograd
+    from mimir_amd.workloads import build_case
+
+    cores = _cores()
+    torch.set_num_threads(cores)
+    n, p = case.seq_lens[0], case.prefixes[0]
+    s0 = int(case.cu_seqlens[0])
+    sl = slice(s0, s0 + n)
+    tens = tuple(t[sl].float().contiguous() for t in (case.q, case.k, case.v, case.dout))
+    sample = build_case(tens, [n], [p], is_causal=case.is_causal)
+    flops = sample.fwd_flops() + sample.bwd_flops()
+
+    def run():
+        q, k, v = (t.clone().requires_grad_(True) for t in sample_tensors)
+        o = dense_forward_autograd(q, k, v, sample.is_causal, *sample.oracle_args())
+        o.backward(sample.dout)
+
+    sample_tensors = (sample.q, sample.k, sample.v)
+    t0 = time.perf_counter()
+    run()  # warm-up
+    first = time.perf_counter() - t0
+    reps = max(1, min(3, int(seconds_cap / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except Exception:  # noqa: BLE001
+        model = "unknown"
+    return {
+        "value": round(flops / sec / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"fwd+bwd of sequence 0 (n={n}, prefix={p}, Hq={case.q.shape[1]}, Hkv={case.k.shape[1]}, "
+                   f"D={case.q.shape[2]}) of the same batch, fp32 torch SDPA with bool mask + autograd, "
+                   f"median of {reps} after 1 warm-up"),
+        "seconds": round(sec, 4),
+        "cpu_model": model,
+        "torch": torch.__version__,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build runs the kernel on one "
+              "GPU's share of the workload; multi-GPU sharding is described in DESIGN.md, not launched.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from mimir_amd import _capi
+    from mimir_amd import prefixlm as P
+    from mimir_amd.workloads import CONFIG_NAMES, bwd_bytes, fwd_bytes, make_config
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    case = make_config(args.workload, seed=args.seed)
+    c = case.to(dev)
+    T, hq, d = c.q.shape
+    hkv = c.k.shape[1]
+    elem = c.q.element_size()
+    scale = 1.0 / math.sqrt(d)
+    lib = _capi.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    fp, out, lse, keep_f = P.prepare_fwd(c.q, c.k, c.v, case.is_causal, c.prefix_lens, c.causal_lens, c.cu_seqlens,
+                                         c.total_seqlen, c.numseqs, c.max_seqlen_all, scale)
+    _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(fp), stream))
+    bp, dq, dk, dv, keep_b = P.prepare_bwd(c.dout, c.q, c.k, c.v, out, lse, case.is_causal, c.prefix_lens,
+                                           c.causal_lens, c.cu_seqlens, c.total_seqlen, c.numseqs,
+                                           c.max_seqlen_all, scale)
+    fwd_only = args.workload == 1
+    stages = [("fwd", None)]
+    if not fwd_only:
+        stages += [("delta", _capi.BWD_STAGE_DELTA), ("dkdv", _capi.BWD_STAGE_DKDV), ("dq", _capi.BWD_STAGE_DQ),
+                   ("fill", _capi.BWD_STAGE_FILL)]
+    fwd_fn, stg_fn = lib.mimir_prefixlm_fwd, lib.mimir_prefixlm_bwd_stages
+    fpr, bpr = ctypes.byref(fp), ctypes.byref(bp)
+
+    def step(evs=None):
+        for i, (name, bits) in enumerate(stages):
+            if evs is not None:
+                evs[i].record()
+            rc = fwd_fn(fpr, stream) if bits is None else stg_fn(bpr, bits, stream)
+            if rc:
+                _capi.raise_for_status(lib, rc)
+        if evs is not None:
+            evs[len(stages)].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(K)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for k in range(K):
+        step(evs[k])
+    t_end.record()
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    ms_per_step = total_ms / K
+    stage_ms = {name: [evs[k][i].elapsed_time(evs[k][i + 1]) for k in range(K)] for i, (name, _) in enumerate(stages)}
+    stage_avg = {name: sum(v) / len(v) for name, v in stage_ms.items()}
+    stage_med = {name: statistics.median(v) for name, v in stage_ms.items()}
+    step_med = statistics.median(sum(stage_ms[n][k] for n, _ in stages) for k in range(K))
+
+    pairs = case.pairs()
+    f_fwd = 4.0 * d * hq * pairs
+    f_bwd = 0.0 if fwd_only else 10.0 * d * hq * pairs
+    flops = f_fwd + f_bwd
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    peak = PEAK_F32_TFLOPS if c.q.dtype == torch.float32 else PEAK_BF16_TFLOPS
+    kernel_flops = {"fwd": f_fwd, "dkdv": 8.0 * d * hq * pairs, "dq": 2.0 * d * hq * pairs}
+    kernel_names = {"fwd": "fwd_bf16_kernel" if elem == 2 else "fwd_f32_kernel", "dkdv": "dkdv_kernel",
+                    "dq": "dq_kernel"}
+    dom = max((n for n in kernel_flops if n in stage_avg), key=lambda n: stage_avg[n])
+    achieved = kernel_flops[dom] / (stage_avg[dom] * 1e-3) / 1e12
+    alg_bytes = fwd_bytes(T, hq, hkv, d, elem) + (0 if fwd_only else bwd_bytes(T, hq, hkv, d, elem))
+
+    res = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if elem == 2 else "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": CONFIG_NAMES[args.workload],
+            "tokens": T, "seqs": len(case.seq_lens), "max_seq_len": max(case.seq_lens),
+            "q_heads": hq, "kv_heads": hkv, "head_dim": d, "seed": args.seed,
+            "attended_pairs": pairs, "passes": "fwd" if fwd_only else "fwd+bwd",
+            "parallelism": "single-gpu",
+        },
+        "pct_of_peak": round(100.0 * value / peak, 2),
+        "hbm_gbs_algorithmic": round(alg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "step_ms_median": round(step_med, 5),
+        "stage_ms_avg": {n: round(v, 5) for n, v in stage_avg.items()},
+        "stage_ms_median": {n: round(v, 5) for n, v in stage_med.items()},
+        "fwd_tflops": round(f_fwd / (stage_avg["fwd"] * 1e-3) / 1e12, 2),
+        "roofline": {
+            "kernel": kernel_names[dom],
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4),
+            "traffic": None,
+            "algorithmic_flops_per_launch": kernel_flops[dom],
+        },
+    }
+    if not fwd_only:
+        bwd_ms = sum(stage_avg[n] for n in ("delta", "dkdv", "dq", "fill"))
+        res["bwd_tflops"] = round(f_bwd / (bwd_ms * 1e-3) / 1e12, 2)
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(case)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

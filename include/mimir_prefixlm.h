@@ -135,6 +135,20 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* params, void* stream);
  * backward src/mimir/model/flash_attention_prefixlm_mps.py:1456-1561. */
 int mimir_prefixlm_bwd(const MimirPrefixLMBwdParams* params, void* stream);
 
+/* Backward stages, for callers that schedule them themselves (e.g. dK/dV and
+ * dQ on two streams once delta is done).  mimir_prefixlm_bwd runs them all, in
+ * order.  DELTA must complete before DKDV and DQ; DKDV, DQ and FILL are
+ * independent of each other.  No reference counterpart: the reference exposes
+ * the backward only through autograd (flash_attention_prefixlm_v2.py:270-283). */
+enum MimirBwdStage {
+  MIMIR_BWD_STAGE_DELTA = 1, /* delta = rowsum(O * dO) into the workspace */
+  MIMIR_BWD_STAGE_DKDV = 2,  /* dK, dV for every key row inside a sequence */
+  MIMIR_BWD_STAGE_DQ = 4,    /* dQ for every active query row */
+  MIMIR_BWD_STAGE_FILL = 8,  /* zero dQ / dK / dV rows outside every sequence */
+  MIMIR_BWD_STAGE_ALL = 15
+};
+int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* params, int stages, void* stream);
+
 /* Bytes of device workspace the backward needs (float32 delta [Hq, T]). */
 size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads);
 

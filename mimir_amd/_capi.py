@@ -66,9 +66,16 @@ class BwdParams(ctypes.Structure):
     ]
 
 
+BWD_STAGE_DELTA = 1
+BWD_STAGE_DKDV = 2
+BWD_STAGE_DQ = 4
+BWD_STAGE_FILL = 8
+BWD_STAGE_ALL = 15
+
 EXPORTED_SYMBOLS = (
     "mimir_prefixlm_fwd",
     "mimir_prefixlm_bwd",
+    "mimir_prefixlm_bwd_stages",
     "mimir_prefixlm_bwd_workspace_bytes",
     "mimir_prefixlm_check_metadata",
     "mimir_prefixlm_last_error",
@@ -101,6 +108,8 @@ def load() -> ctypes.CDLL:
         lib.mimir_prefixlm_fwd.restype = ctypes.c_int
         lib.mimir_prefixlm_bwd.argtypes = [ctypes.POINTER(BwdParams), _vp]
         lib.mimir_prefixlm_bwd.restype = ctypes.c_int
+        lib.mimir_prefixlm_bwd_stages.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int, _vp]
+        lib.mimir_prefixlm_bwd_stages.restype = ctypes.c_int
         lib.mimir_prefixlm_bwd_workspace_bytes.argtypes = [_i32, _i32]
         lib.mimir_prefixlm_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mimir_prefixlm_check_metadata.argtypes = [_vp, _vp, _vp, _i32, _vp, _vp]

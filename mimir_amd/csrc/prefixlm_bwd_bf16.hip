@@ -380,7 +380,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(const BwdArgs a) {
 }
 
 template <int D>
-hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream) {
+hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages) {
   BwdArgs a;
   a.q = (const bf16_t*)p.q;
   a.k = (const bf16_t*)p.k;
@@ -414,25 +414,27 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream) {
   a.scale_log2 = p.softmax_scale * kLog2e;
 
   const int64_t rows = (int64_t)p.total_tokens * p.num_q_heads;
-  if (rows > 0) {
+  if (rows > 0 && (stages & MIMIR_BWD_STAGE_DELTA)) {
     const int64_t threads = rows * (D / 8);
     hipLaunchKernelGGL(delta_kernel<D>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);
   }
   if (p.numseqs > 0 && a.num_q_tiles > 0) {
-    hipLaunchKernelGGL(dkdv_kernel<D>, dim3(p.num_kv_heads, a.num_kv_tiles, p.numseqs), dim3(kThreads), 0,
-                       stream, a);
-    hipLaunchKernelGGL(dq_kernel<D>, dim3(p.num_q_heads, a.num_q_tiles, p.numseqs), dim3(kThreads), 0,
-                       stream, a);
+    if (stages & MIMIR_BWD_STAGE_DKDV)
+      hipLaunchKernelGGL(dkdv_kernel<D>, dim3(p.num_kv_heads, a.num_kv_tiles, p.numseqs), dim3(kThreads), 0,
+                         stream, a);
+    if (stages & MIMIR_BWD_STAGE_DQ)
+      hipLaunchKernelGGL(dq_kernel<D>, dim3(p.num_q_heads, a.num_q_tiles, p.numseqs), dim3(kThreads), 0,
+                         stream, a);
   }
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, hipStream_t stream) {
+hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages) {
   switch (p.head_dim) {
-    case 64: return launch<64>(p, stream);
-    case 128: return launch<128>(p, stream);
+    case 64: return launch<64>(p, stream, stages);
+    case 128: return launch<128>(p, stream, stages);
     default: return hipErrorInvalidValue;
   }
 }

@@ -186,9 +186,14 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* p, void* stream_) {
   return hip_status(e, "forward padding fill");
 }
 
-int mimir_prefixlm_bwd(const MimirPrefixLMBwdParams* p, void* stream_) {
+int mimir_prefixlm_bwd(const MimirPrefixLMBwdParams* p, void* stream) {
+  return mimir_prefixlm_bwd_stages(p, MIMIR_BWD_STAGE_ALL, stream);
+}
+
+int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* p, int stages, void* stream_) {
   g_last_error.clear();
   if (p == nullptr) return fail(MIMIR_ERR_INVALID_ARGUMENT, "params is NULL");
+  if (stages & ~MIMIR_BWD_STAGE_ALL) return fail(MIMIR_ERR_INVALID_ARGUMENT, "unknown backward stage bits");
   hipStream_t stream = (hipStream_t)stream_;
   int rc = check_common(p->dtype, p->total_tokens, p->num_q_heads, p->num_kv_heads, p->head_dim, p->numseqs,
                         p->total_seqlen, p->max_seqlen_all, p->softmax_scale);
@@ -212,8 +217,10 @@ int mimir_prefixlm_bwd(const MimirPrefixLMBwdParams* p, void* stream_) {
   if (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +
                                                 std::to_string(need) + " bytes");
-  hipError_t e = dt == MIMIR_DTYPE_BFLOAT16 ? mimir_launch_bwd_bf16(*p, stream) : mimir_launch_bwd_f32(*p, stream);
+  hipError_t e = dt == MIMIR_DTYPE_BFLOAT16 ? mimir_launch_bwd_bf16(*p, stream, stages)
+                                            : mimir_launch_bwd_f32(*p, stream, stages);
   if ((rc = hip_status(e, "backward launch"))) return rc;
+  if (!(stages & MIMIR_BWD_STAGE_FILL)) return MIMIR_OK;
   const int es = elem_bytes_of(dt);
   e = launch_fill(p->dq, p->dq_stride_token, p->dq_stride_head, nullptr, 0, p->cu_seqlens, p->numseqs,
                   p->total_seqlen, p->total_tokens, p->num_q_heads, D, es, stream);

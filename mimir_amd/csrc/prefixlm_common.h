@@ -135,9 +135,9 @@ __device__ __forceinline__ int swz(int row, int col) {
 
 // Internal launchers (implemented per kernel file, dispatched from prefixlm_capi.cpp).
 hipError_t mimir_launch_fwd_bf16(const MimirPrefixLMFwdParams& p, hipStream_t stream);
-hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, hipStream_t stream);
+hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages);
 hipError_t mimir_launch_fwd_f32(const MimirPrefixLMFwdParams& p, hipStream_t stream);
-hipError_t mimir_launch_bwd_f32(const MimirPrefixLMBwdParams& p, hipStream_t stream);
+hipError_t mimir_launch_bwd_f32(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages);
 hipError_t mimir_launch_fill_fwd_padding(const MimirPrefixLMFwdParams& p, hipStream_t stream);
 hipError_t mimir_launch_fill_bwd_padding(const MimirPrefixLMBwdParams& p, hipStream_t stream);
 hipError_t mimir_launch_check_metadata(const int32_t* prefix_lens, const int32_t* causal_lens,

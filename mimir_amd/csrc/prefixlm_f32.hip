@@ -334,7 +334,7 @@ hipError_t launch_fwd(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
 }
 
 template <int D>
-hipError_t launch_bwd(const MimirPrefixLMBwdParams& p, hipStream_t stream) {
+hipError_t launch_bwd(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages) {
   F32Args a = common_args(p.total_tokens, p.num_q_heads, p.num_kv_heads, p.total_seqlen, p.is_causal,
                           p.softmax_scale, p.prefix_lens, p.cu_seqlens);
   a.q = (const float*)p.q; a.k = (const float*)p.k; a.v = (const float*)p.v;
@@ -352,14 +352,16 @@ hipError_t launch_bwd(const MimirPrefixLMBwdParams& p, hipStream_t stream) {
   a.lse_sh = p.lse_stride_head;
   a.num_tiles = (p.max_seqlen_all + kRowsPerBlock - 1) / kRowsPerBlock;
   const int64_t rows = (int64_t)p.total_tokens * p.num_q_heads;
-  if (rows > 0)
+  if (rows > 0 && (stages & MIMIR_BWD_STAGE_DELTA))
     hipLaunchKernelGGL(delta_f32_kernel<D>, dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
                        dim3(256), 0, stream, a);
   if (a.num_tiles > 0 && p.numseqs > 0) {
-    hipLaunchKernelGGL(dq_f32_kernel<D>, dim3(p.num_q_heads, a.num_tiles, p.numseqs), dim3(kThreads), 0,
-                       stream, a);
-    hipLaunchKernelGGL(dkdv_f32_kernel<D>, dim3(p.num_kv_heads, a.num_tiles, p.numseqs), dim3(kThreads), 0,
-                       stream, a);
+    if (stages & MIMIR_BWD_STAGE_DQ)
+      hipLaunchKernelGGL(dq_f32_kernel<D>, dim3(p.num_q_heads, a.num_tiles, p.numseqs), dim3(kThreads), 0,
+                         stream, a);
+    if (stages & MIMIR_BWD_STAGE_DKDV)
+      hipLaunchKernelGGL(dkdv_f32_kernel<D>, dim3(p.num_kv_heads, a.num_tiles, p.numseqs), dim3(kThreads), 0,
+                         stream, a);
   }
   return hipGetLastError();
 }
@@ -378,12 +380,12 @@ hipError_t mimir_launch_fwd_f32(const MimirPrefixLMFwdParams& p, hipStream_t str
   }
 }
 
-hipError_t mimir_launch_bwd_f32(const MimirPrefixLMBwdParams& p, hipStream_t stream) {
+hipError_t mimir_launch_bwd_f32(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages) {
   switch (p.head_dim) {
-    case 32: return launch_bwd<32>(p, stream);
-    case 64: return launch_bwd<64>(p, stream);
-    case 96: return launch_bwd<96>(p, stream);
-    case 128: return launch_bwd<128>(p, stream);
+    case 32: return launch_bwd<32>(p, stream, stages);
+    case 64: return launch_bwd<64>(p, stream, stages);
+    case 96: return launch_bwd<96>(p, stream, stages);
+    case 128: return launch_bwd<128>(p, stream, stages);
     default: return hipErrorInvalidValue;
   }
 }

@@ -118,10 +118,6 @@ def _geometry(q: Tensor, k: Tensor, v: Tensor):
     return q.shape[0], hq, hkv, q.shape[2]
 
 
-def _ptr(t: Optional[Tensor]) -> Optional[int]:
-    return None if t is None else t.data_ptr()
-
-
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -148,9 +144,13 @@ def check_metadata(prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
         raise ValueError(f"Bad PrefixLM lengths for sequence {s}: {p} + {c} != {length}")
 
 
-def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
-              softmax_scale):
-    lib = _capi.load()
+def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
+                softmax_scale):
+    """Validate, allocate O / lse and fill the C parameter struct of the forward.
+
+    Returns ``(params, out, lse, keep)``; ``keep`` holds every tensor the struct
+    points to and must outlive the launch.
+    """
     for name, t in (("q", q), ("k", k), ("v", v)):
         _check_device_tensor(name, t)
     T, hq, hkv, d = _geometry(q, k, v)
@@ -172,13 +172,27 @@ def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_se
         T, hq, hkv, d, n, _scalar(total_seqlen), _scalar(max_seqlen_all), int(bool(is_causal)),
         _DTYPES[q.dtype], float(softmax_scale),
     )
-    _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), _stream(device)))
+    return p, out, lse, (q, k, v, pl, cl, cu)
+
+
+def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
+              softmax_scale):
+    lib = _capi.load()
+    p, out, lse, keep = prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
+                                    numseqs, max_seqlen_all, softmax_scale)
+    _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), _stream(out.device)))
     return out, lse
 
 
-def _bwd_impl(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-              max_seqlen_all, softmax_scale):
+def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+                max_seqlen_all, softmax_scale):
+    """Validate, allocate dQ / dK / dV and the workspace, fill the backward struct.
+
+    Returns ``(params, dq, dk, dv, keep)``.
+    """
     lib = _capi.load()
+    for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout)):
+        _check_device_tensor(name, t)
     T, hq, hkv, d = _geometry(q, k, v)
     n = _scalar(numseqs)
     device = q.device
@@ -194,7 +208,7 @@ def _bwd_impl(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_s
     dk = torch.empty((T, hkv, d), dtype=q.dtype, device=device)
     dv = torch.empty((T, hkv, d), dtype=q.dtype, device=device)
     ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_bytes(T, hq))
-    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=device)
+    ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
     p = _capi.BwdParams(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(), lse.data_ptr(),
         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
@@ -206,7 +220,15 @@ def _bwd_impl(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_s
         T, hq, hkv, d, n, _scalar(total_seqlen), _scalar(max_seqlen_all), int(bool(is_causal)),
         _DTYPES[q.dtype], float(softmax_scale), ws.data_ptr(), ws_bytes,
     )
-    _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd(ctypes.byref(p), _stream(device)))
+    return p, dq, dk, dv, (q, k, v, out, dout, lse, pl, cl, cu, ws)
+
+
+def _bwd_impl(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+              max_seqlen_all, softmax_scale):
+    lib = _capi.load()
+    p, dq, dk, dv, keep = prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens,
+                                      total_seqlen, numseqs, max_seqlen_all, softmax_scale)
+    _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd(ctypes.byref(p), _stream(dq.device)))
     return dq, dk, dv
 
 
