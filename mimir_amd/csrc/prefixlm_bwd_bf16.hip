@@ -13,6 +13,10 @@
 //           The GQA reduction over the q-heads of one kv head happens in
 //           registers, so no kernel needs atomics and results are deterministic.
 //
+// Both tile loops stream their operand tiles with direct buffer-to-LDS loads
+// into two LDS stages (one barrier per tile).  Grids are ordered so that the
+// heaviest tiles of every sequence are dispatched first.
+//
 // Math: dV = P^T dO, dP = dO V^T, delta = rowsum(dO * O), dS = P (dP - delta) * scale,
 // dQ = dS K, dK = dS^T Q  (flash_attention_prefixlm_mps.py:1601-1675), with the GQA
 // head map of flash_attention_prefixlm_dense.py:10-16 (q head h -> kv head h / G).
@@ -21,11 +25,12 @@
 namespace {
 using namespace mimir;
 
-constexpr int kThreads = 256;
-constexpr int kBlockQ = 128;  // dq: query rows per workgroup (32 per wave)
-constexpr int kBlockK = 64;   // dq: keys per LDS tile
-constexpr int kBlockKV = 128; // dkdv: keys per workgroup (32 per wave)
-constexpr int kBlockQT = 64;  // dkdv: query rows per LDS tile
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kBlockQ = 128;   // dq: query rows per workgroup (32 per wave)
+constexpr int kBlockK = 64;    // dq: keys per LDS tile
+constexpr int kBlockKV = 128;  // dkdv: keys per workgroup (32 per wave)
+constexpr int kBlockQT = 64;   // dkdv: query rows per LDS tile
 
 struct BwdArgs {
   const bf16_t* q;
@@ -44,6 +49,7 @@ struct BwdArgs {
   int64_t dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh, lse_sh;
   int T;
   int Hq;
+  int Hkv;
   int group;
   int total_seqlen;
   int is_causal;
@@ -53,22 +59,18 @@ struct BwdArgs {
   float scale_log2;
 };
 
-__device__ __forceinline__ uint32_t rows_bytes(int rows, int64_t stride, int d) {
-  return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + d) * 2) : 0u;
-}
-
 // ---------------------------------------------------------------------------
 // delta = rowsum(O * dO), one (token, head) row per D/8 lanes.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void delta_kernel(const BwdArgs a) {
   constexpr int LPR = D / 8;  // lanes per row
-  const int gid = blockIdx.x * 256 + threadIdx.x;
-  const int row = gid / LPR;  // row = t * Hq + h
-  const int c = gid % LPR;
-  const bool valid = row < a.T * a.Hq;
-  const int t = valid ? row / a.Hq : 0;
-  const int h = valid ? row % a.Hq : 0;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / LPR;  // row = t * Hq + h
+  const int c = (int)(gid % LPR);
+  const bool valid = row < (int64_t)a.T * a.Hq;
+  const int t = valid ? (int)(row / a.Hq) : 0;
+  const int h = valid ? (int)(row % a.Hq) : 0;
   float acc = 0.f;
   if (valid) {
     const bf16x8 ov = *(const bf16x8*)&a.o[(int64_t)t * a.o_st + (int64_t)h * a.o_sh + c * 8];
@@ -85,24 +87,27 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdArgs a) {
 // dQ.  Mirrors the forward's S^T formulation: each lane owns one query column,
 // so lse and delta are lane-local and dS^T feeds the B operand of dQ^T += K^T dS^T
 // directly; K^T fragments come from the row-major K tile via ds_read_b64_tr_b16.
+// Grid: x = sequence * Hq + head, y = query tile (reversed: longest key ranges first).
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(kThreads, 1) void dq_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   constexpr int DT = D / 32;
   constexpr int KS = D / 16;
-  constexpr int CPR = D / 8;
-  constexpr int LOADS = kBlockK * CPR / kThreads;
-  __shared__ __attribute__((aligned(16))) bf16_t sK[kBlockK * D];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[kBlockK * D];
+  using L = TileLayout<D>;
+  static_assert(kBlockK == 64, "one TileLayout tile per K / V block");
+  __shared__ __attribute__((aligned(16))) bf16_t sK0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sK1[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV1[L::kElems];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-  const int h = blockIdx.x;
+  const int h = blockIdx.x % a.Hq;
+  const int s = blockIdx.x / a.Hq;
   const int qtile = a.num_q_tiles - 1 - (int)blockIdx.y;
-  const int s = blockIdx.z;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = qtile * kBlockQ;
   if (m0 >= g.nq) return;
@@ -126,6 +131,12 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(const BwdArgs a) {
   const __amdgpu_buffer_rsrc_t rv =
       make_rsrc(a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh, rows_bytes(g.n, a.v_st, D));
 
+  auto issue = [&](int kt, bf16_t* tk, bf16_t* tv) {
+    lds_tile_async<D, kWaves>(rk, a.k_st, kt * kBlockK, tk, wave, lane);
+    lds_tile_async<D, kWaves>(rv, a.v_st, kt * kBlockK, tv, wave, lane);
+  };
+  issue(0, sK0, sV0);
+
   bf16x8 qf[KS], dof[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -142,22 +153,11 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(const BwdArgs a) {
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
   const float c2 = a.scale_log2;
-  const int tj = lane & 15, tg = lane >> 4, t_hi = tg >> 1, t_dh = tg & 1;
+  const TileLanes<D> tl(lane);
 
-  for (int kt = 0; kt < nkt; ++kt) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int idx = tid + i * kThreads;
-      const int row = idx / CPR, c = idx % CPR;
-      const int key = kt * kBlockK + row;
-      *(i32x4*)&sK[swz<D>(row, c * 8)] = buf_load16(rk, (uint32_t)(((int64_t)key * a.k_st + c * 8) * 2));
-      *(i32x4*)&sV[swz<D>(row, c * 8)] = buf_load16(rv, (uint32_t)(((int64_t)key * a.v_st + c * 8) * 2));
-    }
-    __syncthreads();
+  auto compute = [&](int kt, const bf16_t* sK, const bf16_t* sV) {
     const int kb = kt * kBlockK;
-    if (!wave_active || kb >= w_kend_max) continue;
-
+    if (!wave_active || kb >= w_kend_max) return;
     f32x16 st[2], dpt[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
@@ -165,8 +165,9 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(const BwdArgs a) {
       dpt[mt] = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 kf = *(const bf16x8*)&sK[swz<D>(32 * mt + l32, 16 * ks + 8 * hi)];
-        const bf16x8 vf = *(const bf16x8*)&sV[swz<D>(32 * mt + l32, 16 * ks + 8 * hi)];
+        const int o = tl.op_base + mt * 32 * L::kRowElems + ks * 16;
+        const bf16x8 kf = *(const bf16x8*)&sK[o];
+        const bf16x8 vf = *(const bf16x8*)&sV[o];
         st[mt] = mfma32(kf, qf[ks], st[mt]);
         dpt[mt] = mfma32(vf, dof[ks], dpt[mt]);
       }
@@ -192,15 +193,26 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(const BwdArgs a) {
     }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const int col = 32 * dt + 16 * t_dh + 4 * (tj & 3);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const int krow = 16 * kk + 4 * t_hi + (tj >> 2);
-        const bf16x4 k0 = lds_read_tr16(&sK[swz<D>(krow, col)]);
-        const bf16x4 k1 = lds_read_tr16(&sK[swz<D>(krow + 8, col)]);
+        const bf16_t* kp = &sK[tl.tr_base + kk * 16 * L::kRowElems + dt * 32];
+        const bf16x4 k0 = lds_read_tr16(kp);
+        const bf16x4 k1 = lds_read_tr16(kp + 8 * L::kRowElems);
         dqacc[dt] = mfma32(cat8(k0, k1), sf[kk], dqacc[dt]);
       }
     }
+  };
+
+  for (int kt = 0; kt < nkt; kt += 2) {
+    wait_vmem();
+    __syncthreads();
+    if (kt + 1 < nkt) issue(kt + 1, sK1, sV1);
+    compute(kt, sK0, sV0);
+    if (kt + 1 >= nkt) break;
+    wait_vmem();
+    __syncthreads();
+    if (kt + 2 < nkt) issue(kt + 2, sK0, sV0);
+    compute(kt + 1, sK1, sV1);
   }
 
   if (!wave_active || qpos >= g.nq) return;
@@ -222,26 +234,33 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(const BwdArgs a) {
 // dV^T += dO^T P and dK^T += Q^T dS directly, and the transposed dO^T / Q^T
 // fragments come from the row-major LDS tiles via ds_read_b64_tr_b16.
 // The query range starts at qstart(first key) = (key < p ? 0 : key).
+// Grid: x = sequence * Hkv + kv head, y = key tile (prefix keys, the heaviest, first).
 // ---------------------------------------------------------------------------
+// Two waves per SIMD fit the register budget at head_dim 64; at 128 the K / V
+// fragments plus the dK / dV accumulators need one wave per SIMD.
 template <int D>
-__global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(kThreads, D <= 64 ? 2 : 1) void dkdv_kernel(const BwdArgs a) {
   constexpr int DT = D / 32;
   constexpr int KS = D / 16;
-  constexpr int CPR = D / 8;
-  constexpr int LOADS = kBlockQT * CPR / kThreads;
-  __shared__ __attribute__((aligned(16))) bf16_t sQ[kBlockQT * D];
-  __shared__ __attribute__((aligned(16))) bf16_t sdO[kBlockQT * D];
-  __shared__ __attribute__((aligned(16))) float sL[kBlockQT];
-  __shared__ __attribute__((aligned(16))) float sD[kBlockQT];
+  using L = TileLayout<D>;
+  static_assert(kBlockQT == 64, "one TileLayout tile per Q / dO block");
+  __shared__ __attribute__((aligned(16))) bf16_t sQ0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sO0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sQ1[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sO1[L::kElems];
+  __shared__ __attribute__((aligned(16))) float sL0[kBlockQT];
+  __shared__ __attribute__((aligned(16))) float sD0[kBlockQT];
+  __shared__ __attribute__((aligned(16))) float sL1[kBlockQT];
+  __shared__ __attribute__((aligned(16))) float sD1[kBlockQT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-  const int hk = blockIdx.x;
+  const int hk = blockIdx.x % a.Hkv;
+  const int s = blockIdx.x / a.Hkv;
   const int ktile = blockIdx.y;
-  const int s = blockIdx.z;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int kb0 = ktile * kBlockKV;
   if (kb0 >= g.n) return;
@@ -254,11 +273,36 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(const BwdArgs a) {
   const int w_qs_max = qstart_of(g.p, ka + 31);
   const int q_begin = qstart_of(g.p, kb0);
   const int nqt = g.nq > q_begin ? (g.nq - q_begin + kBlockQT - 1) / kBlockQT : 0;
+  const int n_iter = nqt * a.group;  // (q head, query tile) pairs
 
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(
       a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh, rows_bytes(g.n, a.k_st, D));
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(
       a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh, rows_bytes(g.n, a.v_st, D));
+
+  // Iteration it covers q head hk * G + it / nqt and query tile it % nqt.
+  auto issue = [&](int it, bf16_t* tq, bf16_t* to, float* tl, float* td) {
+    const int hh = it / nqt;
+    const int qb = q_begin + (it - hh * nqt) * kBlockQT;
+    const int h = hk * a.group + hh;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+        a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, rows_bytes(g.nq, a.q_st, D));
+    const __amdgpu_buffer_rsrc_t rdo = make_rsrc(
+        a.dout + (int64_t)g.start * a.do_st + (int64_t)h * a.do_sh, rows_bytes(g.nq, a.do_st, D));
+    lds_tile_async<D, kWaves>(rq, a.q_st, qb, tq, wave, lane);
+    lds_tile_async<D, kWaves>(rdo, a.do_st, qb, to, wave, lane);
+    if (wave == 0) {
+      const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse + (int64_t)h * a.lse_sh + g.start, (uint32_t)g.nq * 4u);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (__attribute__((address_space(3))) void*)tl, 4,
+                                               (uint32_t)(qb + lane) * 4u, 0, 0, 0);
+    } else if (wave == 1) {
+      const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.delta + (int64_t)h * a.T + g.start, (uint32_t)g.nq * 4u);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (__attribute__((address_space(3))) void*)td, 4,
+                                               (uint32_t)(qb + lane) * 4u, 0, 0, 0);
+    }
+  };
+  if (n_iter > 0) issue(0, sQ0, sO0, sL0, sD0);
+
   bf16x8 kf[KS], vf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -273,92 +317,78 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(const BwdArgs a) {
     dvacc[dt] = f32x16{};
   }
   const float c2 = a.scale_log2;
-  const int tj = lane & 15, tg = lane >> 4, t_hi = tg >> 1, t_dh = tg & 1;
+  const TileLanes<D> tl(lane);
 
-  for (int hh = 0; hh < a.group; ++hh) {
-    const int h = hk * a.group + hh;
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
-        a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, rows_bytes(g.nq, a.q_st, D));
-    const __amdgpu_buffer_rsrc_t rdo = make_rsrc(
-        a.dout + (int64_t)g.start * a.do_st + (int64_t)h * a.do_sh, rows_bytes(g.nq, a.do_st, D));
-    const float* lse_h = a.lse + (int64_t)h * a.lse_sh + g.start;
-    const float* dl_h = a.delta + (int64_t)h * a.T + g.start;
-
-    for (int qt = 0; qt < nqt; ++qt) {
-      const int qb = q_begin + qt * kBlockQT;
-      __syncthreads();
+  auto compute = [&](int it, const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
+    const int hh = it / nqt;
+    const int qb = q_begin + (it - hh * nqt) * kBlockQT;
+    if (!wave_active || qb + kBlockQT <= w_qs_min) return;
+    const bool masked = (qb < w_qs_max) || (qb + kBlockQT > g.nq);
 #pragma unroll
-      for (int i = 0; i < LOADS; ++i) {
-        const int idx = tid + i * kThreads;
-        const int row = idx / CPR, c = idx % CPR;
-        const int qr = qb + row;
-        *(i32x4*)&sQ[swz<D>(row, c * 8)] = buf_load16(rq, (uint32_t)(((int64_t)qr * a.q_st + c * 8) * 2));
-        *(i32x4*)&sdO[swz<D>(row, c * 8)] = buf_load16(rdo, (uint32_t)(((int64_t)qr * a.do_st + c * 8) * 2));
+    for (int mt = 0; mt < 2; ++mt) {
+      f32x16 sc = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int o = tl.op_base + mt * 32 * L::kRowElems + ks * 16;
+        const bf16x8 qa8 = *(const bf16x8*)&sQ[o];
+        const bf16x8 da8 = *(const bf16x8*)&sdO[o];
+        sc = mfma32(qa8, kf[ks], sc);
+        dp = mfma32(da8, vf[ks], dp);
       }
-      if (tid < kBlockQT) {
-        const int qr = qb + tid;
-        const bool ok = qr < g.nq;
-        sL[tid] = ok ? lse_h[qr] * kLog2e : 0.f;
-        sD[tid] = ok ? dl_h[qr] : 0.f;
+      // rows of sc / dp: query 32*mt + 8*(r/4) + 4*hi + r%4 ; column: this lane's key
+      f32x16 pm, ds;
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int qr0 = 32 * mt + 8 * rg + 4 * hi;
+        const f32x4 l4 = *(const f32x4*)&sL[qr0];
+        const f32x4 d4 = *(const f32x4*)&sD[qr0];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * rg + e;
+          float pr = fast_exp2(__builtin_fmaf(sc[r], c2, -l4[e] * kLog2e));
+          if (masked) {
+            const int qp = qb + qr0 + e;
+            if (qp < qs_lane || qp >= g.nq) pr = 0.f;
+          }
+          pm[r] = pr;
+          ds[r] = pr * (dp[r] - d4[e]);
+        }
       }
-      __syncthreads();
-      if (!wave_active || qb + kBlockQT <= w_qs_min) continue;
-      const bool masked = (qb < w_qs_max) || (qb + kBlockQT > g.nq);
-
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        f32x16 sc = f32x16{}, dp = f32x16{};
+      for (int s2 = 0; s2 < 2; ++s2) {
+        f32x8 tp, tds;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const bf16x8 qa8 = *(const bf16x8*)&sQ[swz<D>(32 * mt + l32, 16 * ks + 8 * hi)];
-          const bf16x8 da8 = *(const bf16x8*)&sdO[swz<D>(32 * mt + l32, 16 * ks + 8 * hi)];
-          sc = mfma32(qa8, kf[ks], sc);
-          dp = mfma32(da8, vf[ks], dp);
+        for (int e = 0; e < 8; ++e) {
+          tp[e] = pm[8 * s2 + e];
+          tds[e] = ds[8 * s2 + e];
         }
-        // rows of sc / dp: query 32*mt + 8*(r/4) + 4*hi + r%4 ; column: this lane's key
-        f32x16 pm, ds;
+        const bf16x8 pb = to_bf16x8(tp);
+        const bf16x8 db = to_bf16x8(tds);
+        const int kk = 2 * mt + s2;  // 16-query step inside the 64-row tile
 #pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
-          const int qr0 = 32 * mt + 8 * rg + 4 * hi;
-          const f32x4 l4 = *(const f32x4*)&sL[qr0];
-          const f32x4 d4 = *(const f32x4*)&sD[qr0];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * rg + e;
-            float pr = fast_exp2(__builtin_fmaf(sc[r], c2, -l4[e]));
-            if (masked) {
-              const int qp = qb + qr0 + e;
-              if (qp < qs_lane || qp >= g.nq) pr = 0.f;
-            }
-            pm[r] = pr;
-            ds[r] = pr * (dp[r] - d4[e]);
-          }
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          f32x8 tp, tds;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            tp[e] = pm[8 * s2 + e];
-            tds[e] = ds[8 * s2 + e];
-          }
-          const bf16x8 pb = to_bf16x8(tp);
-          const bf16x8 db = to_bf16x8(tds);
-          const int kk = 2 * mt + s2;  // 16-query step inside the 64-row tile
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const int col = 32 * dt + 16 * t_dh + 4 * (tj & 3);
-            const int qrow = 16 * kk + 4 * t_hi + (tj >> 2);
-            const bf16x4 o0 = lds_read_tr16(&sdO[swz<D>(qrow, col)]);
-            const bf16x4 o1 = lds_read_tr16(&sdO[swz<D>(qrow + 8, col)]);
-            dvacc[dt] = mfma32(cat8(o0, o1), pb, dvacc[dt]);
-            const bf16x4 q0 = lds_read_tr16(&sQ[swz<D>(qrow, col)]);
-            const bf16x4 q1 = lds_read_tr16(&sQ[swz<D>(qrow + 8, col)]);
-            dkacc[dt] = mfma32(cat8(q0, q1), db, dkacc[dt]);
-          }
+        for (int dt = 0; dt < DT; ++dt) {
+          const int o = tl.tr_base + kk * 16 * L::kRowElems + dt * 32;
+          const bf16x4 o0 = lds_read_tr16(&sdO[o]);
+          const bf16x4 o1 = lds_read_tr16(&sdO[o + 8 * L::kRowElems]);
+          dvacc[dt] = mfma32(cat8(o0, o1), pb, dvacc[dt]);
+          const bf16x4 q0 = lds_read_tr16(&sQ[o]);
+          const bf16x4 q1 = lds_read_tr16(&sQ[o + 8 * L::kRowElems]);
+          dkacc[dt] = mfma32(cat8(q0, q1), db, dkacc[dt]);
         }
       }
     }
+  };
+
+  for (int it = 0; it < n_iter; it += 2) {
+    wait_vmem();
+    __syncthreads();
+    if (it + 1 < n_iter) issue(it + 1, sQ1, sO1, sL1, sD1);
+    compute(it, sQ0, sO0, sL0, sD0);
+    if (it + 1 >= n_iter) break;
+    wait_vmem();
+    __syncthreads();
+    if (it + 2 < n_iter) issue(it + 2, sQ0, sO0, sL0, sD0);
+    compute(it + 1, sQ1, sO1, sL1, sD1);
   }
 
   if (!wave_active || kpos >= g.n) return;
@@ -405,6 +435,7 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stage
   a.lse_sh = p.lse_stride_head;
   a.T = p.total_tokens;
   a.Hq = p.num_q_heads;
+  a.Hkv = p.num_kv_heads;
   a.group = p.num_q_heads / p.num_kv_heads;
   a.total_seqlen = p.total_seqlen;
   a.is_causal = p.is_causal;
@@ -420,10 +451,10 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stage
   }
   if (p.numseqs > 0 && a.num_q_tiles > 0) {
     if (stages & MIMIR_BWD_STAGE_DKDV)
-      hipLaunchKernelGGL(dkdv_kernel<D>, dim3(p.num_kv_heads, a.num_kv_tiles, p.numseqs), dim3(kThreads), 0,
+      hipLaunchKernelGGL(dkdv_kernel<D>, dim3(p.num_kv_heads * p.numseqs, a.num_kv_tiles), dim3(kThreads), 0,
                          stream, a);
     if (stages & MIMIR_BWD_STAGE_DQ)
-      hipLaunchKernelGGL(dq_kernel<D>, dim3(p.num_q_heads, a.num_q_tiles, p.numseqs), dim3(kThreads), 0,
+      hipLaunchKernelGGL(dq_kernel<D>, dim3(p.num_q_heads * p.numseqs, a.num_q_tiles), dim3(kThreads), 0,
                          stream, a);
   }
   return hipGetLastError();

@@ -70,6 +70,12 @@ __device__ __forceinline__ SeqGeom load_seq(const int32_t* __restrict__ cu_seqle
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
+// Bytes covering rows [0, rows) of a bf16 matrix with row stride `stride`
+// elements whose rows hold `d` values: the num_records of a per-sequence resource.
+__device__ __forceinline__ uint32_t rows_bytes(int rows, int64_t stride, int d) {
+  return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + d) * 2) : 0u;
+}
+
 __device__ __forceinline__ i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
 }
@@ -121,15 +127,81 @@ __device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
 
 __device__ __forceinline__ bf16x8 to_bf16x8(f32x8 v) { return __builtin_convertvector(v, bf16x8); }
 
-// 16-byte-chunk XOR swizzle of a row-major [rows][D] bf16 tile in LDS: chunk c of
-// row r lives at chunk (c ^ (r & 7)).  Keeps the 32x16 MFMA operand reads and the
-// 4-row transposing reads free of bank conflicts.
+// ---------------------------------------------------------------------------
+// LDS tile layout.  A [64][D] bf16 operand tile is stored with
+//   * a row stride of D/8 + 1 sixteen-byte units (one unit of padding), and
+//   * logical row k at physical row perm(k), which moves bits (2 1 0) of k to
+//     (0 2 1): rows 4i..4i+3 land on physical rows of one parity, two apart.
+// With 64 banks x 4 bytes, a 16-lane phase of an MFMA operand read (16 rows,
+// one unit each) touches unit (perm(k) * (D/8 + 1) + c) mod 16 -- sixteen
+// distinct values -- and a 16-lane phase of ds_read_b64_tr_b16 (rows 4i..4i+3,
+// two adjacent units) touches eight distinct units: both are conflict-free.
+// Because the layout is a row permutation plus padding, every per-k-step /
+// per-d-tile displacement is a compile-time constant (an instruction offset).
+// ---------------------------------------------------------------------------
 template <int D>
-__device__ __forceinline__ int swz(int row, int col) {
-  // col in elements; returns element offset inside the tile
-  const int chunk = (col >> 3) ^ (row & 7);
-  return row * D + (chunk << 3) + (col & 7);
+struct TileLayout {
+  static constexpr int kUnits = D / 8;           // 16-byte units of data per row
+  static constexpr int kRowUnits = kUnits + 1;   // with padding
+  static constexpr int kRowElems = kRowUnits * 8;
+  static constexpr int kElems = 64 * kRowElems;  // one 64-row tile
+  __device__ static constexpr int perm(int k) { return (k & ~7) | ((k & 3) << 1) | ((k >> 2) & 1); }
+  __device__ static constexpr int unperm(int r) { return (r & ~7) | ((r & 1) << 2) | ((r >> 1) & 3); }
+  // element offset of (logical row k, column d)
+  __device__ static constexpr int off(int k, int d) { return perm(k) * kRowElems + d; }
+};
+
+// Asynchronous global -> LDS copy of rows [r0, r0 + 64) of a bf16 matrix with row
+// stride `st` elements (relative to the buffer resource base) into a TileLayout
+// tile, with buffer_load_dwordx4 ... lds.  One wave instruction writes 64
+// consecutive 16-byte units of LDS in lane order, so the layout is produced on
+// the global side: the lane owning physical unit u loads logical row
+// unperm(u / kRowUnits), unit u % kRowUnits; padding units read zeros from an
+// out-of-range offset.  Rows outside the resource read as zeros too.
+// Completion is tracked by vmcnt; callers wait before the barrier that
+// publishes the tile.
+template <int D, int NWAVES>
+__device__ __forceinline__ void lds_tile_async(__amdgpu_buffer_rsrc_t rsrc, int64_t st, int r0, bf16_t* tile,
+                                               int wave, int lane) {
+  using L = TileLayout<D>;
+  constexpr int NINST = L::kRowUnits;  // 64 rows * kRowUnits units / 64 lanes
+#pragma unroll
+  for (int i = 0; i < (NINST + NWAVES - 1) / NWAVES; ++i) {
+    const int g = i * NWAVES + wave;
+    if (g < NINST) {
+      const int u = g * 64 + lane;
+      const int prow = u / L::kRowUnits;
+      const int c = u - prow * L::kRowUnits;
+      const int k = L::unperm(prow);
+      const uint32_t off =
+          c < L::kUnits ? (uint32_t)(((int64_t)(r0 + k) * st + c * 8) * 2) : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, (__attribute__((address_space(3))) void*)(tile + g * 512), 16, off, 0, 0, 0);
+    }
+  }
 }
+
+// Lane geometry of the operand reads from a TileLayout tile.
+//  * MFMA 32x32x16 operand with rows on lanes (A of K Q^T, Q K^T, ...): lane
+//    reads logical row 32*mt + (lane & 31), columns 16*ks + 8*(lane >> 5) .. +7:
+//    element offset op_base + mt * 32 * kRowElems + ks * 16.
+//  * transposed operand (ds_read_b64_tr_b16) over rows 16*kk + 4*(lane >> 5) +
+//    0..3 (and + 8), columns 32*dt + 16*((lane >> 4) & 1) + 0..15: element offset
+//    tr_base + kk * 16 * kRowElems + dt * 32 (+ 8 * kRowElems for the second read).
+template <int D>
+struct TileLanes {
+  using L = TileLayout<D>;
+  int op_base;
+  int tr_base;
+  __device__ explicit TileLanes(int lane) {
+    op_base = L::off(lane & 31, 8 * (lane >> 5));
+    const int tj = lane & 15, tg = lane >> 4;
+    tr_base = L::off(4 * (tg >> 1) + (tj >> 2), 16 * (tg & 1) + 4 * (tj & 3));
+  }
+};
+
+// s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 }  // namespace mimir
 

@@ -34,7 +34,7 @@ struct F32Args {
   const int32_t* cu_seqlens;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, do_st, do_sh;
   int64_t dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh, lse_sh;
-  int T, Hq, group, total_seqlen, is_causal, num_tiles;
+  int T, Hq, Hkv, group, total_seqlen, is_causal, num_tiles;
   float scale, scale_log2;
 };
 
@@ -85,9 +85,9 @@ __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
   constexpr int EPL = D / 4;
   __shared__ __attribute__((aligned(16))) float sK[kTile * D];
   __shared__ __attribute__((aligned(16))) float sV[kTile * D];
-  const int h = blockIdx.x;
+  const int h = blockIdx.x % a.Hq;
+  const int s = blockIdx.x / a.Hq;
   const int tile = a.num_tiles - 1 - (int)blockIdx.y;
-  const int s = blockIdx.z;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = tile * kRowsPerBlock;
   if (m0 >= g.nq) return;
@@ -174,9 +174,9 @@ __global__ __launch_bounds__(kThreads) void dq_f32_kernel(const F32Args a) {
   constexpr int EPL = D / 4;
   __shared__ __attribute__((aligned(16))) float sK[kTile * D];
   __shared__ __attribute__((aligned(16))) float sV[kTile * D];
-  const int h = blockIdx.x;
+  const int h = blockIdx.x % a.Hq;
+  const int s = blockIdx.x / a.Hq;
   const int tile = a.num_tiles - 1 - (int)blockIdx.y;
-  const int s = blockIdx.z;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = tile * kRowsPerBlock;
   if (m0 >= g.nq) return;
@@ -233,9 +233,9 @@ __global__ __launch_bounds__(kThreads) void dkdv_f32_kernel(const F32Args a) {
   __shared__ __attribute__((aligned(16))) float sO[kTile * D];
   __shared__ float sL[kTile];
   __shared__ float sD[kTile];
-  const int hk = blockIdx.x;
+  const int hk = blockIdx.x % a.Hkv;
+  const int s = blockIdx.x / a.Hkv;
   const int tile = blockIdx.y;
-  const int s = blockIdx.z;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int k0 = tile * kRowsPerBlock;
   if (k0 >= g.n) return;
@@ -305,6 +305,7 @@ F32Args common_args(int T, int Hq, int Hkv, int total_seqlen, int is_causal, flo
   F32Args a = {};
   a.T = T;
   a.Hq = Hq;
+  a.Hkv = Hkv;
   a.group = Hq / Hkv;
   a.total_seqlen = total_seqlen;
   a.is_causal = is_causal;
@@ -328,7 +329,7 @@ hipError_t launch_fwd(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
   a.lse_sh = p.lse_stride_head;
   a.num_tiles = (p.max_seqlen_all + kRowsPerBlock - 1) / kRowsPerBlock;
   if (a.num_tiles == 0 || p.numseqs == 0) return hipSuccess;
-  hipLaunchKernelGGL(fwd_f32_kernel<D>, dim3(p.num_q_heads, a.num_tiles, p.numseqs), dim3(kThreads), 0,
+  hipLaunchKernelGGL(fwd_f32_kernel<D>, dim3(p.num_q_heads * p.numseqs, a.num_tiles), dim3(kThreads), 0,
                      stream, a);
   return hipGetLastError();
 }
@@ -357,10 +358,10 @@ hipError_t launch_bwd(const MimirPrefixLMBwdParams& p, hipStream_t stream, int s
                        dim3(256), 0, stream, a);
   if (a.num_tiles > 0 && p.numseqs > 0) {
     if (stages & MIMIR_BWD_STAGE_DQ)
-      hipLaunchKernelGGL(dq_f32_kernel<D>, dim3(p.num_q_heads, a.num_tiles, p.numseqs), dim3(kThreads), 0,
+      hipLaunchKernelGGL(dq_f32_kernel<D>, dim3(p.num_q_heads * p.numseqs, a.num_tiles), dim3(kThreads), 0,
                          stream, a);
     if (stages & MIMIR_BWD_STAGE_DKDV)
-      hipLaunchKernelGGL(dkdv_f32_kernel<D>, dim3(p.num_kv_heads, a.num_tiles, p.numseqs), dim3(kThreads), 0,
+      hipLaunchKernelGGL(dkdv_f32_kernel<D>, dim3(p.num_kv_heads * p.numseqs, a.num_tiles), dim3(kThreads), 0,
                          stream, a);
   }
   return hipGetLastError();

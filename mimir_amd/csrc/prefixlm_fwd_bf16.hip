@@ -1,15 +1,16 @@
 // bf16 prefix-LM attention forward for gfx950 (MI355X).
 //
 // One workgroup = 4 waves = 128 query rows of one (sequence, query head); each
-// wave owns 32 rows.  The kernel computes S^T = K Q^T on v_mfma_f32_32x32x16_bf16
+// wave owns 32 rows.  Grid: x = sequence * Hq + head, y = query tile counted from
+// the end of the sequence, so the tiles with the longest key ranges go first.  The kernel computes S^T = K Q^T on v_mfma_f32_32x32x16_bf16
 // so that every lane holds one query column of the score tile: the softmax
 // max/sum over keys is a per-lane reduction plus one v_permlane32_swap, the
 // running max / sum / rescale factor are lane-local, and the probabilities
 // P^T leave the accumulator already in the B-operand layout of O^T += V^T P^T.
 // V^T fragments come straight from the row-major V tile through
 // ds_read_b64_tr_b16.  K/V tiles of 64 keys are staged in LDS (XOR-swizzled
-// 16-byte chunks); the next tile is prefetched into registers while the current
-// one is consumed.
+// 16-byte chunks) by direct buffer-to-LDS loads, double-buffered so that tile
+// t + 1 streams in while tile t is consumed, with one barrier per tile.
 //
 // Tile classes follow the mask algebra j < kend(i) = max(p, i + 1): key tiles at
 // or beyond a wave's largest kend are skipped, tiles entirely below its smallest
@@ -37,6 +38,7 @@ struct FwdArgs {
   const int32_t* cu_seqlens;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_sh;
   int T;             // packed length
+  int Hq;
   int group;         // Hq / Hkv
   int total_seqlen;
   int is_causal;
@@ -45,21 +47,19 @@ struct FwdArgs {
   float scale_log2;  // softmax scale * log2(e)
 };
 
-__device__ __forceinline__ uint32_t rows_bytes(int rows, int64_t stride, int d) {
-  // bytes covering rows [0, rows) of a [rows][stride] bf16 matrix whose rows hold d values
-  return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + d) * 2) : 0u;
-}
-
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) {
-  constexpr int DT = D / 32;   // 32-row d tiles of O^T
-  constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
-  constexpr int CPR = D / 8;   // 16-byte chunks per row
-  constexpr int LOADS = kBlockN * CPR / kThreads;  // 16-byte chunks per thread per tile
-  static_assert(LOADS * kThreads == kBlockN * CPR, "tile load split");
+  constexpr int DT = D / 32;  // 32-row d tiles of O^T
+  constexpr int KS = D / 16;  // k-steps of S^T = K Q^T
 
-  __shared__ __attribute__((aligned(16))) bf16_t sK[kBlockN * D];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[kBlockN * D];
+  // Two LDS stages of one K tile and one V tile each.  Separate objects let the
+  // compiler see that reads of one stage never alias the loads into the other.
+  using L = TileLayout<D>;
+  static_assert(kBlockN == 64, "one TileLayout tile per K / V block");
+  __shared__ __attribute__((aligned(16))) bf16_t sK0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sK1[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV1[L::kElems];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -67,9 +67,9 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
-  const int h = blockIdx.x;
+  const int h = blockIdx.x % a.Hq;
+  const int s = blockIdx.x / a.Hq;
   const int mtile = a.num_m_tiles - 1 - (int)blockIdx.y;  // longest key ranges first
-  const int s = blockIdx.z;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = mtile * kBlockM;
   if (m0 >= g.nq) return;
@@ -86,12 +86,18 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
   const int qpos = qa + l32;
   const int kend_lane = kend_of(g.p, qpos);
 
-  const bf16_t* qbase = a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh;
-  const bf16_t* kbase_p = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
-  const bf16_t* vbase_p = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(qbase, rows_bytes(g.nq, a.q_st, D));
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase_p, rows_bytes(g.n, a.k_st, D));
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase_p, rows_bytes(g.n, a.v_st, D));
+  const __amdgpu_buffer_rsrc_t rq =
+      make_rsrc(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, rows_bytes(g.nq, a.q_st, D));
+  const __amdgpu_buffer_rsrc_t rk =
+      make_rsrc(a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh, rows_bytes(g.n, a.k_st, D));
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh, rows_bytes(g.n, a.v_st, D));
+
+  auto issue = [&](int kt, bf16_t* tk, bf16_t* tv) {
+    lds_tile_async<D, kWaves>(rk, a.k_st, kt * kBlockN, tk, wave, lane);
+    lds_tile_async<D, kWaves>(rv, a.v_st, kt * kBlockN, tv, wave, lane);
+  };
+  issue(0, sK0, sV0);
 
   // Q^T B-operand fragments: lane holds query qpos, d = 16*ks + 8*hi .. +7.
   bf16x8 qf[KS];
@@ -101,30 +107,6 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
     qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, off));
   }
 
-  // Global -> register prefetch of one K/V tile.
-  i32x4 pk[LOADS], pv[LOADS];
-  auto load_tile = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int idx = tid + i * kThreads;
-      const int row = idx / CPR;
-      const int c = idx % CPR;
-      const int key = kt * kBlockN + row;
-      pk[i] = buf_load16(rk, (uint32_t)(((int64_t)key * a.k_st + c * 8) * 2));
-      pv[i] = buf_load16(rv, (uint32_t)(((int64_t)key * a.v_st + c * 8) * 2));
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int idx = tid + i * kThreads;
-      const int row = idx / CPR;
-      const int c = idx % CPR;
-      *(i32x4*)&sK[swz<D>(row, c * 8)] = pk[i];
-      *(i32x4*)&sV[swz<D>(row, c * 8)] = pv[i];
-    }
-  };
-
   f32x16 oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
@@ -132,21 +114,11 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
   float l_run = 0.f;
   const float c2 = a.scale_log2;
 
-  // lane geometry of the transposing V reads
-  const int tj = lane & 15;
-  const int tg = lane >> 4;
-  const int t_hi = tg >> 1;
-  const int t_dh = tg & 1;
+  const TileLanes<D> tl(lane);
 
-  load_tile(0);
-  for (int kt = 0; kt < nkt; ++kt) {
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (kt + 1 < nkt) load_tile(kt + 1);
-
+  auto compute = [&](int kt, const bf16_t* sK, const bf16_t* sV) {
     const int kb = kt * kBlockN;
-    if (!wave_active || kb >= w_kend_max) continue;
+    if (!wave_active || kb >= w_kend_max) return;
 
     // S^T = K Q^T for 64 keys: two 32-key sub-tiles.
     f32x16 st[2];
@@ -155,7 +127,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
       st[mt] = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 kf = *(const bf16x8*)&sK[swz<D>(32 * mt + l32, 16 * ks + 8 * hi)];
+        const bf16x8 kf = *(const bf16x8*)&sK[tl.op_base + mt * 32 * L::kRowElems + ks * 16];
         st[mt] = mfma32(kf, qf[ks], st[mt]);
       }
     }
@@ -176,15 +148,21 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
     mx = xor32_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    if (__builtin_amdgcn_ballot_w64(m_new > m_run) != 0) {
+    // Lazy rescaling: the reference max only moves when the running max grows by
+    // more than 2^8 in probability terms (always on the first tile, where m_run is
+    // -inf).  In between, probabilities stay below 256, exact in fp32 and in bf16's
+    // range; the final 1/l uses the same reference, so the result is unchanged.
+    const float m_cand = fmaxf(m_run, mx);
+    const bool grow = (m_cand - m_run) * c2 > 8.f;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = grow ? m_cand : m_run;
       const float alpha = fast_exp2((m_run - m_new) * c2);
       l_run *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      m_run = m_new;
     }
-    m_run = m_new;
-    const float mb = m_new * c2;
+    const float mb = m_run * c2;
 
     float lsum = 0.f;
 #pragma unroll
@@ -210,15 +188,26 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
 
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const int col = 32 * dt + 16 * t_dh + 4 * (tj & 3);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const int krow = 16 * kk + 4 * t_hi + (tj >> 2);
-        const bf16x4 v0 = lds_read_tr16(&sV[swz<D>(krow, col)]);
-        const bf16x4 v1 = lds_read_tr16(&sV[swz<D>(krow + 8, col)]);
+        const bf16_t* vp = &sV[tl.tr_base + kk * 16 * L::kRowElems + dt * 32];
+        const bf16x4 v0 = lds_read_tr16(vp);
+        const bf16x4 v1 = lds_read_tr16(vp + 8 * L::kRowElems);
         oacc[dt] = mfma32(cat8(v0, v1), pf[kk], oacc[dt]);
       }
     }
+  };
+
+  for (int kt = 0; kt < nkt; kt += 2) {
+    wait_vmem();
+    __syncthreads();
+    if (kt + 1 < nkt) issue(kt + 1, sK1, sV1);
+    compute(kt, sK0, sV0);
+    if (kt + 1 >= nkt) break;
+    wait_vmem();
+    __syncthreads();
+    if (kt + 2 < nkt) issue(kt + 2, sK0, sV0);
+    compute(kt + 1, sK1, sV1);
   }
 
   if (!wave_active) return;
@@ -256,6 +245,7 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
   a.o_st = p.out_stride_token; a.o_sh = p.out_stride_head;
   a.lse_sh = p.lse_stride_head;
   a.T = p.total_tokens;
+  a.Hq = p.num_q_heads;
   a.group = p.num_q_heads / p.num_kv_heads;
   a.total_seqlen = p.total_seqlen;
   a.is_causal = p.is_causal;
@@ -263,7 +253,8 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
   a.scale = p.softmax_scale;
   a.scale_log2 = p.softmax_scale * kLog2e;
   if (a.num_m_tiles == 0 || p.numseqs == 0) return hipSuccess;
-  dim3 grid(p.num_q_heads, a.num_m_tiles, p.numseqs);
+  // x = sequence * Hq + head (GQA siblings adjacent), y = query tile, heaviest first
+  dim3 grid(p.num_q_heads * p.numseqs, a.num_m_tiles);
   hipLaunchKernelGGL(fwd_bf16_kernel<D>, grid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
