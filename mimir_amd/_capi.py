@@ -10,10 +10,12 @@ codes onto the exception types the reference raises for the same conditions
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmimir_prefixlm.so"
+# MIMIR_PREFIXLM_LIB overrides the in-tree library (e.g. to A/B two builds).
+LIB_PATH = Path(os.environ.get("MIMIR_PREFIXLM_LIB") or Path(__file__).resolve().parent / "_lib" / "libmimir_prefixlm.so")
 ABI_VERSION = 1
 
 DTYPE_FLOAT32 = 0

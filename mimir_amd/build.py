@@ -38,6 +38,8 @@ SOURCES = [
     "prefixlm_capi.hip",
     "prefixlm_fwd_bf16.hip",
     "prefixlm_bwd_bf16.hip",
+    "prefixlm_bwd_dq_bf16.hip",
+    "prefixlm_bwd_dkdv_bf16.hip",
     "prefixlm_f32.hip",
 ]
 

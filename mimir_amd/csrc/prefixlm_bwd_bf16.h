@@ -1,0 +1,45 @@
+// Shared argument block and launchers of the bf16 backward kernels
+// (prefixlm_bwd_bf16.hip: delta + orchestration, prefixlm_bwd_dq_bf16.hip: dQ,
+// prefixlm_bwd_dkdv_bf16.hip: dK / dV).
+#pragma once
+
+#include "prefixlm_common.h"
+
+namespace mimir {
+
+constexpr int kBwdBlockQT = 64;  // query rows per LDS tile in dK / dV
+
+struct BwdArgs {
+  const bf16_t* q;
+  const bf16_t* k;
+  const bf16_t* v;
+  const bf16_t* o;
+  const bf16_t* dout;
+  const float* lse;
+  bf16_t* dq;
+  bf16_t* dk;
+  bf16_t* dv;
+  float* delta;
+  const int32_t* prefix_lens;
+  const int32_t* cu_seqlens;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, do_st, do_sh;
+  int64_t dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh, lse_sh;
+  int T;
+  int Hq;
+  int Hkv;
+  int group;
+  int total_seqlen;
+  int is_causal;
+  int num_tiles;     // grid y extent of the launched kernel
+  float scale;
+  float scale_log2;
+};
+
+
+// Each launcher computes its own grid from the geometry in `a` and enqueues one
+// kernel on `stream`.
+hipError_t launch_bwd_dq_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all, hipStream_t stream);
+hipError_t launch_bwd_dkdv_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all,
+                                hipStream_t stream);
+
+}  // namespace mimir

@@ -1,0 +1,176 @@
+// bf16 prefix-LM attention backward, dQ kernel, for gfx950 (MI355X).
+// Owner = (query head, 128 query rows); see prefixlm_bwd_bf16.hip for the split.
+#include "prefixlm_bwd_bf16.h"
+
+namespace mimir {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kBlockQ = 128;  // query rows per workgroup (32 per wave)
+constexpr int kBlockK = 64;   // keys per LDS tile
+
+// ---------------------------------------------------------------------------
+// dQ.  Mirrors the forward's S^T formulation: each lane owns one query column,
+// so lse and delta are lane-local and dS^T feeds the B operand of dQ^T += K^T dS^T
+// directly; K^T fragments come from the row-major K tile via ds_read_b64_tr_b16.
+// Grid: x = sequence * Hq + head, y = query tile (reversed: longest key ranges first).
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
+  constexpr int DT = D / 32;
+  constexpr int KS = D / 16;
+  using L = TileLayout<D>;
+  static_assert(kBlockK == 64, "one TileLayout tile per K / V block");
+  __shared__ __attribute__((aligned(16))) bf16_t sK0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sK1[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV1[L::kElems];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hi = lane >> 5;
+  const int h = blockIdx.x % a.Hq;
+  const int s = blockIdx.x / a.Hq;
+  const int qtile = a.num_tiles - 1 - (int)blockIdx.y;
+  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const int m0 = qtile * kBlockQ;
+  if (m0 >= g.nq) return;
+  const int hk = h / a.group;
+
+  const int wg_kend = max(g.p, min(m0 + kBlockQ, g.nq));
+  const int nkt = (wg_kend + kBlockK - 1) / kBlockK;
+  const int qa = m0 + wave * 32;
+  const bool wave_active = qa < g.nq;
+  const int w_kend_max = wave_active ? max(g.p, min(qa + 32, g.nq)) : 0;
+  const int w_kend_min = max(g.p, qa + 1);
+  const int qpos = qa + l32;
+  const int kend_lane = kend_of(g.p, qpos);
+
+  const __amdgpu_buffer_rsrc_t rq =
+      make_rsrc(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, rows_bytes(g.nq, a.q_st, D));
+  const __amdgpu_buffer_rsrc_t rdo = make_rsrc(
+      a.dout + (int64_t)g.start * a.do_st + (int64_t)h * a.do_sh, rows_bytes(g.nq, a.do_st, D));
+  const bf16_t* kseq = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
+  const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
+  const TileLoader<D, kWaves> ldk(a.k_st, wave, lane), ldv(a.v_st, wave, lane);
+
+  auto issue = [&](int kt, bf16_t* tk, bf16_t* tv) {
+    ldk.issue(kseq, kt * kBlockK, g.n, tk);
+    ldv.issue(vseq, kt * kBlockK, g.n, tv);
+  };
+  issue(0, sK0, sV0);
+
+  bf16x8 qf[KS], dof[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(((int64_t)qpos * a.q_st + 16 * ks + 8 * hi) * 2)));
+    dof[ks] = __builtin_bit_cast(bf16x8, buf_load16(rdo, (uint32_t)(((int64_t)qpos * a.do_st + 16 * ks + 8 * hi) * 2)));
+  }
+  float lse2 = 0.f, dlt = 0.f;
+  if (qpos < g.nq) {
+    lse2 = a.lse[(int64_t)h * a.lse_sh + g.start + qpos] * kLog2e;
+    dlt = a.delta[(int64_t)h * a.T + g.start + qpos];
+  }
+
+  f32x16 dqacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
+  const float c2 = a.scale_log2;
+  const TileLanes<D> tl(lane);
+
+  auto compute = [&](int kt, const bf16_t* sK, const bf16_t* sV) {
+    const int kb = kt * kBlockK;
+    if (!wave_active || kb >= w_kend_max) return;
+    f32x16 st[2], dpt[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      st[mt] = f32x16{};
+      dpt[mt] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int o = tl.op_base + mt * 32 * L::kRowElems + ks * 16;
+        const bf16x8 kf = *(const bf16x8*)&sK[o];
+        const bf16x8 vf = *(const bf16x8*)&sV[o];
+        st[mt] = mfma32(kf, qf[ks], st[mt]);
+        dpt[mt] = mfma32(vf, dof[ks], dpt[mt]);
+      }
+    }
+    const bool masked = kb + kBlockK > w_kend_min;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kpos = kb + 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
+        float pr = fast_exp2(__builtin_fmaf(st[mt][r], c2, -lse2));
+        if (masked && kpos >= kend_lane) pr = 0.f;
+        st[mt][r] = pr * (dpt[mt][r] - dlt);
+      }
+    bf16x8 sf[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int mt = kk >> 1, s8 = (kk & 1) * 8;
+      f32x8 t;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = st[mt][s8 + e];
+      sf[kk] = to_bf16x8(t);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16_t* kp = &sK[tl.tr_base + kk * 16 * L::kRowElems + dt * 32];
+        const bf16x4 k0 = lds_read_tr16(kp);
+        const bf16x4 k1 = lds_read_tr16(kp + L::kTrSecond);
+        dqacc[dt] = mfma32(cat8(k0, k1), sf[kk], dqacc[dt]);
+      }
+    }
+  };
+
+  for (int kt = 0; kt < nkt; kt += 2) {
+    wait_vmem();
+    __syncthreads();
+    if (kt + 1 < nkt) issue(kt + 1, sK1, sV1);
+    compute(kt, sK0, sV0);
+    if (kt + 1 >= nkt) break;
+    wait_vmem();
+    __syncthreads();
+    if (kt + 2 < nkt) issue(kt + 2, sK0, sV0);
+    compute(kt + 1, sK1, sV1);
+  }
+
+  if (!wave_active || qpos >= g.nq) return;
+  bf16_t* drow = a.dq + (int64_t)(g.start + qpos) * a.dq_st + (int64_t)h * a.dq_sh;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      f32x4 t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = dqacc[dt][4 * rg + e] * a.scale;
+      *(bf16x4*)&drow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
+    }
+}
+
+
+template <int D>
+hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
+  a.num_tiles = (max_seqlen_all + kBlockQ - 1) / kBlockQ;
+  if (numseqs <= 0 || a.num_tiles == 0) return hipSuccess;
+  hipLaunchKernelGGL(dq_kernel<D>, dim3(a.Hq * numseqs, a.num_tiles), dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_bwd_dq_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all, hipStream_t stream) {
+  switch (head_dim) {
+    case 64: return launch<64>(a, numseqs, max_seqlen_all, stream);
+    case 128: return launch<128>(a, numseqs, max_seqlen_all, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace mimir

@@ -130,14 +130,16 @@ __device__ __forceinline__ bf16x8 to_bf16x8(f32x8 v) { return __builtin_convertv
 // ---------------------------------------------------------------------------
 // LDS tile layout.  A [64][D] bf16 operand tile is stored with
 //   * a row stride of D/8 + 1 sixteen-byte units (one unit of padding), and
-//   * logical row k at physical row perm(k), which moves bits (2 1 0) of k to
-//     (0 2 1): rows 4i..4i+3 land on physical rows of one parity, two apart.
-// With 64 banks x 4 bytes, a 16-lane phase of an MFMA operand read (16 rows,
-// one unit each) touches unit (perm(k) * (D/8 + 1) + c) mod 16 -- sixteen
-// distinct values -- and a 16-lane phase of ds_read_b64_tr_b16 (rows 4i..4i+3,
-// two adjacent units) touches eight distinct units: both are conflict-free.
-// Because the layout is a row permutation plus padding, every per-k-step /
-// per-d-tile displacement is a compile-time constant (an instruction offset).
+//   * logical row k at physical row perm(k), which transposes the 4 x 4 grid
+//     of each 16-row block: k = 16 b + 4 i + j -> 16 b + 4 j + i.
+// With 64 banks x 4 bytes (16 units), an MFMA operand read serves 16 lanes per
+// cycle (16 rows of one block, one unit each) and touches units
+// (perm(k) * (D/8 + 1) + c) mod 16: sixteen distinct values.  A transposing
+// ds_read_b64_tr_b16 serves 32 lanes per cycle: rows 4i..4i+3 of one block, which
+// land on physical rows i, i+4, i+8, i+12, each read at 4 adjacent units -- again
+// sixteen distinct units.  Both patterns are therefore conflict-free, and since
+// the layout is a row permutation plus padding, every per-k-step / per-d-tile
+// displacement is a compile-time constant (an instruction offset).
 // ---------------------------------------------------------------------------
 template <int D>
 struct TileLayout {
@@ -145,41 +147,58 @@ struct TileLayout {
   static constexpr int kRowUnits = kUnits + 1;   // with padding
   static constexpr int kRowElems = kRowUnits * 8;
   static constexpr int kElems = 64 * kRowElems;  // one 64-row tile
-  __device__ static constexpr int perm(int k) { return (k & ~7) | ((k & 3) << 1) | ((k >> 2) & 1); }
-  __device__ static constexpr int unperm(int r) { return (r & ~7) | ((r & 1) << 2) | ((r >> 1) & 3); }
+  // perm is an involution (a 4 x 4 transpose), so unperm == perm
+  __device__ static constexpr int perm(int k) { return (k & ~15) | ((k & 3) << 2) | ((k >> 2) & 3); }
+  __device__ static constexpr int unperm(int r) { return perm(r); }
   // element offset of (logical row k, column d)
   __device__ static constexpr int off(int k, int d) { return perm(k) * kRowElems + d; }
+  // rows x and x + 8 (x < 8) of a block sit two physical rows apart
+  static constexpr int kTrSecond = 2 * kRowElems;
 };
 
-// Asynchronous global -> LDS copy of rows [r0, r0 + 64) of a bf16 matrix with row
-// stride `st` elements (relative to the buffer resource base) into a TileLayout
-// tile, with buffer_load_dwordx4 ... lds.  One wave instruction writes 64
-// consecutive 16-byte units of LDS in lane order, so the layout is produced on
-// the global side: the lane owning physical unit u loads logical row
-// unperm(u / kRowUnits), unit u % kRowUnits; padding units read zeros from an
-// out-of-range offset.  Rows outside the resource read as zeros too.
-// Completion is tracked by vmcnt; callers wait before the barrier that
-// publishes the tile.
+// Asynchronous global -> LDS copy of 64 consecutive rows of a bf16 matrix (row
+// stride `st` elements) into a TileLayout tile, with buffer_load_dwordx4 ... lds.
+// One wave instruction writes 64 consecutive 16-byte units of LDS in lane order,
+// so the layout is produced on the global side: the lane owning physical unit u
+// loads logical row unperm(u / kRowUnits), unit u % kRowUnits; padding units
+// read zeros from an out-of-range offset.  The per-lane byte offsets relative to
+// the tile's first row never change, so they are computed once; each tile only
+// rebuilds the (scalar) buffer resource, whose base is the tile's first row and
+// whose size covers the rows still inside the sequence -- rows beyond it read as
+// zeros.  The kRowUnits wave instructions of a tile are spread over the NWAVES
+// waves; a wave left without one of its own repeats the last instruction (the
+// same data to the same place).  Completion is tracked by vmcnt; callers wait
+// before the barrier that publishes the tile.
 template <int D, int NWAVES>
-__device__ __forceinline__ void lds_tile_async(__amdgpu_buffer_rsrc_t rsrc, int64_t st, int r0, bf16_t* tile,
-                                               int wave, int lane) {
+struct TileLoader {
   using L = TileLayout<D>;
-  constexpr int NINST = L::kRowUnits;  // 64 rows * kRowUnits units / 64 lanes
+  static constexpr int kInst = L::kRowUnits;  // 64 rows * kRowUnits units / 64 lanes
+  static constexpr int kPerWave = (kInst + NWAVES - 1) / NWAVES;
+  uint32_t voff[kPerWave];
+  int lds[kPerWave];  // element offset of each instruction's 1 KiB (wave-uniform)
+  int64_t st;
+
+  __device__ __forceinline__ TileLoader(int64_t stride, int wave, int lane) : st(stride) {
 #pragma unroll
-  for (int i = 0; i < (NINST + NWAVES - 1) / NWAVES; ++i) {
-    const int g = i * NWAVES + wave;
-    if (g < NINST) {
+    for (int i = 0; i < kPerWave; ++i) {
+      const int g = min(i * NWAVES + wave, kInst - 1);
       const int u = g * 64 + lane;
       const int prow = u / L::kRowUnits;
       const int c = u - prow * L::kRowUnits;
       const int k = L::unperm(prow);
-      const uint32_t off =
-          c < L::kUnits ? (uint32_t)(((int64_t)(r0 + k) * st + c * 8) * 2) : 0x80000000u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsrc, (__attribute__((address_space(3))) void*)(tile + g * 512), 16, off, 0, 0, 0);
+      voff[i] = c < L::kUnits ? (uint32_t)((k * st + c * 8) * 2) : 0x80000000u;
+      lds[i] = g * 512;
     }
   }
-}
+  // Copy rows [row0, row0 + 64) of the matrix at `base`; rows >= nrows read as 0.
+  __device__ __forceinline__ void issue(const bf16_t* base, int row0, int nrows, bf16_t* tile) const {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base + (int64_t)row0 * st, rows_bytes(nrows - row0, st, D));
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(tile + lds[i]), 16,
+                                               voff[i], 0, 0, 0);
+  }
+};
 
 // Lane geometry of the operand reads from a TileLayout tile.
 //  * MFMA 32x32x16 operand with rows on lanes (A of K Q^T, Q K^T, ...): lane
@@ -187,7 +206,7 @@ __device__ __forceinline__ void lds_tile_async(__amdgpu_buffer_rsrc_t rsrc, int6
 //    element offset op_base + mt * 32 * kRowElems + ks * 16.
 //  * transposed operand (ds_read_b64_tr_b16) over rows 16*kk + 4*(lane >> 5) +
 //    0..3 (and + 8), columns 32*dt + 16*((lane >> 4) & 1) + 0..15: element offset
-//    tr_base + kk * 16 * kRowElems + dt * 32 (+ 8 * kRowElems for the second read).
+//    tr_base + kk * 16 * kRowElems + dt * 32 (+ kTrSecond for the second read).
 template <int D>
 struct TileLanes {
   using L = TileLayout<D>;

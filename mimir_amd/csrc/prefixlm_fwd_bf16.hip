@@ -2,15 +2,17 @@
 //
 // One workgroup = 4 waves = 128 query rows of one (sequence, query head); each
 // wave owns 32 rows.  Grid: x = sequence * Hq + head, y = query tile counted from
-// the end of the sequence, so the tiles with the longest key ranges go first.  The kernel computes S^T = K Q^T on v_mfma_f32_32x32x16_bf16
-// so that every lane holds one query column of the score tile: the softmax
-// max/sum over keys is a per-lane reduction plus one v_permlane32_swap, the
-// running max / sum / rescale factor are lane-local, and the probabilities
-// P^T leave the accumulator already in the B-operand layout of O^T += V^T P^T.
-// V^T fragments come straight from the row-major V tile through
-// ds_read_b64_tr_b16.  K/V tiles of 64 keys are staged in LDS (XOR-swizzled
-// 16-byte chunks) by direct buffer-to-LDS loads, double-buffered so that tile
-// t + 1 streams in while tile t is consumed, with one barrier per tile.
+// the end of the sequence, so the tiles with the longest key ranges go first.
+//
+// The kernel computes S^T = K Q^T on v_mfma_f32_32x32x16_bf16 so that every lane
+// holds one query column of the score tile: the softmax max/sum over keys is a
+// per-lane reduction plus one v_permlane32_swap, the running max / sum / rescale
+// factor are lane-local, and the probabilities P^T leave the accumulator already
+// in the B-operand layout of O^T += V^T P^T.  V^T fragments come straight from
+// the row-major V tile through ds_read_b64_tr_b16.  K/V tiles of 64 keys are
+// staged in LDS (TileLayout: padded, row-permuted, bank-conflict-free) by direct
+// buffer-to-LDS loads, double-buffered so that tile t + 1 streams in while tile
+// t is consumed, with one barrier per tile.
 //
 // Tile classes follow the mask algebra j < kend(i) = max(p, i + 1): key tiles at
 // or beyond a wave's largest kend are skipped, tiles entirely below its smallest
@@ -63,7 +65,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
@@ -88,14 +90,13 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
 
   const __amdgpu_buffer_rsrc_t rq =
       make_rsrc(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, rows_bytes(g.nq, a.q_st, D));
-  const __amdgpu_buffer_rsrc_t rk =
-      make_rsrc(a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh, rows_bytes(g.n, a.k_st, D));
-  const __amdgpu_buffer_rsrc_t rv =
-      make_rsrc(a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh, rows_bytes(g.n, a.v_st, D));
+  const bf16_t* kseq = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
+  const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
+  const TileLoader<D, kWaves> ldk(a.k_st, wave, lane), ldv(a.v_st, wave, lane);
 
   auto issue = [&](int kt, bf16_t* tk, bf16_t* tv) {
-    lds_tile_async<D, kWaves>(rk, a.k_st, kt * kBlockN, tk, wave, lane);
-    lds_tile_async<D, kWaves>(rv, a.v_st, kt * kBlockN, tv, wave, lane);
+    ldk.issue(kseq, kt * kBlockN, g.n, tk);
+    ldv.issue(vseq, kt * kBlockN, g.n, tv);
   };
   issue(0, sK0, sV0);
 
@@ -116,9 +117,11 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
 
   const TileLanes<D> tl(lane);
 
-  auto compute = [&](int kt, const bf16_t* sK, const bf16_t* sV) {
+  // One 64-key tile; `masked` selects the element-wise mask (tiles that reach
+  // past some row's kend).  A compile-time split into masked / unmasked bodies
+  // was measured: the extra code copies push head_dim 128 over 256 VGPRs.
+  auto compute = [&](bool masked, int kt, const bf16_t* sK, const bf16_t* sV) {
     const int kb = kt * kBlockN;
-    if (!wave_active || kb >= w_kend_max) return;
 
     // S^T = K Q^T for 64 keys: two 32-key sub-tiles.
     f32x16 st[2];
@@ -132,7 +135,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
       }
     }
 
-    if (kb + kBlockN > w_kend_min) {
+    if (masked) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -192,22 +195,28 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
       for (int kk = 0; kk < 4; ++kk) {
         const bf16_t* vp = &sV[tl.tr_base + kk * 16 * L::kRowElems + dt * 32];
         const bf16x4 v0 = lds_read_tr16(vp);
-        const bf16x4 v1 = lds_read_tr16(vp + 8 * L::kRowElems);
+        const bf16x4 v1 = lds_read_tr16(vp + L::kTrSecond);
         oacc[dt] = mfma32(cat8(v0, v1), pf[kk], oacc[dt]);
       }
     }
+  };
+
+  auto step = [&](int kt, const bf16_t* sK, const bf16_t* sV) {
+    const int kb = kt * kBlockN;
+    if (!wave_active || kb >= w_kend_max) return;
+    compute(kb + kBlockN > w_kend_min, kt, sK, sV);
   };
 
   for (int kt = 0; kt < nkt; kt += 2) {
     wait_vmem();
     __syncthreads();
     if (kt + 1 < nkt) issue(kt + 1, sK1, sV1);
-    compute(kt, sK0, sV0);
+    step(kt, sK0, sV0);
     if (kt + 1 >= nkt) break;
     wait_vmem();
     __syncthreads();
     if (kt + 2 < nkt) issue(kt + 2, sK0, sV0);
-    compute(kt + 1, sK1, sV1);
+    step(kt + 1, sK1, sV1);
   }
 
   if (!wave_active) return;
