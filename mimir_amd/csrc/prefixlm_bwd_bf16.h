@@ -31,6 +31,7 @@ struct BwdArgs {
   int total_seqlen;
   int is_causal;
   int num_tiles;     // grid y extent of the launched kernel
+  int grid_x;        // valid blockIdx.x values of the launched kernel
   float scale;
   float scale_log2;
 };

@@ -51,6 +51,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
+  if ((int)blockIdx.x >= a.grid_x) return;
   const int hk = blockIdx.x % a.Hkv;
   const int s = blockIdx.x / a.Hkv;
   const int ktile = blockIdx.y;
@@ -226,7 +227,9 @@ hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream
   constexpr int kDkKeys = DkCfg<D>::kKeys, kDkWaves = DkCfg<D>::kWaves;
   a.num_tiles = (max_seqlen_all + kDkKeys - 1) / kDkKeys;
   if (numseqs <= 0 || a.num_tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL(dkdv_kernel<D>, dim3(a.Hkv * numseqs, a.num_tiles), dim3(kDkWaves * 64), 0, stream, a);
+  a.grid_x = a.Hkv * numseqs;
+  hipLaunchKernelGGL(dkdv_kernel<D>, dim3(xcd_spread_width(a.grid_x), a.num_tiles), dim3(kDkWaves * 64), 0,
+                     stream, a);
   return hipGetLastError();
 }
 

@@ -32,6 +32,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
+  if ((int)blockIdx.x >= a.grid_x) return;
   const int h = blockIdx.x % a.Hq;
   const int s = blockIdx.x / a.Hq;
   const int qtile = a.num_tiles - 1 - (int)blockIdx.y;
@@ -159,7 +160,8 @@ template <int D>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   a.num_tiles = (max_seqlen_all + kBlockQ - 1) / kBlockQ;
   if (numseqs <= 0 || a.num_tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL(dq_kernel<D>, dim3(a.Hq * numseqs, a.num_tiles), dim3(kThreads), 0, stream, a);
+  a.grid_x = a.Hq * numseqs;
+  hipLaunchKernelGGL(dq_kernel<D>, dim3(xcd_spread_width(a.grid_x), a.num_tiles), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

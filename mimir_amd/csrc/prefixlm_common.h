@@ -43,6 +43,13 @@ struct SeqGeom {
   int p;      // effective prefix length, clamped to [0, n]; 0 when is_causal
 };
 
+// Grid x extent for `n` (sequence, head) work columns.  Workgroups are dealt to
+// the 8 XCDs round-robin by linear id, so with an even row width every column
+// would keep all of its tiles (rows) on one XCD -- whole sequences of heavy
+// prefix tiles pile up on half of the XCDs.  An odd width rotates each row by
+// one XCD; the padding column exits at once.
+inline unsigned xcd_spread_width(int n) { return (unsigned)(n | 1); }
+
 // Sequence bounds are clamped to the packed length T so that malformed metadata
 // can never address memory outside the [T, ...] tensors.
 __device__ __forceinline__ SeqGeom load_seq(const int32_t* __restrict__ cu_seqlens,

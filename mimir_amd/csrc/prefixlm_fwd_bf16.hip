@@ -45,6 +45,7 @@ struct FwdArgs {
   int total_seqlen;
   int is_causal;
   int num_m_tiles;
+  int grid_x;        // valid blockIdx.x values: Hq * numseqs
   float scale;       // softmax scale
   float scale_log2;  // softmax scale * log2(e)
 };
@@ -69,6 +70,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
+  if ((int)blockIdx.x >= a.grid_x) return;
   const int h = blockIdx.x % a.Hq;
   const int s = blockIdx.x / a.Hq;
   const int mtile = a.num_m_tiles - 1 - (int)blockIdx.y;  // longest key ranges first
@@ -263,7 +265,8 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
   a.scale_log2 = p.softmax_scale * kLog2e;
   if (a.num_m_tiles == 0 || p.numseqs == 0) return hipSuccess;
   // x = sequence * Hq + head (GQA siblings adjacent), y = query tile, heaviest first
-  dim3 grid(p.num_q_heads * p.numseqs, a.num_m_tiles);
+  a.grid_x = p.num_q_heads * p.numseqs;
+  dim3 grid(xcd_spread_width(a.grid_x), a.num_m_tiles);
   hipLaunchKernelGGL(fwd_bf16_kernel<D>, grid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
