@@ -96,6 +96,25 @@ def cpu_baseline(case, seconds_cap: float = 30.0) -> dict:
     }
 
 
+def copy_calibration(torch, dev, mib: int, reps: int) -> int:
+    """Copy ``mib`` MiB device-to-device ``reps`` times: each launch reads and writes exactly mib MiB."""
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    print(json.dumps({"copy_mib": mib, "bytes_read": n * 4, "bytes_written": n * 4, "launches": reps + 1,
+                      "ms_per_copy": round(ms, 5), "gbs_read_plus_write": round(2 * n * 4 / ms / 1e6, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +123,9 @@ def main() -> int:
     ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="instead of the step, time a plain device copy of this many MiB (reference kernel of known "
+                         "HBM traffic for scaling the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build runs the kernel on one "
@@ -121,6 +143,8 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.copy_calibration_mib > 0:
+        return copy_calibration(torch, dev, args.copy_calibration_mib, max(1, args.steps))
     case = make_config(args.workload, seed=args.seed)
     c = case.to(dev)
     T, hq, d = c.q.shape

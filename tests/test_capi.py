@@ -1,0 +1,144 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point
+include/mimir_prefixlm.h declares, the ctypes structs match the C layout, and
+argument validation fails with the reference's exception types before any
+device work is enqueued."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+from pathlib import Path
+
+import pytest
+
+from mimir_amd import _capi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mimir_prefixlm.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _capi.LIB_PATH.exists():
+        from mimir_amd.build import build
+
+        build(verbose=False)
+    return _capi.load()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\**\s+\**(mimir_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_binding_symbols():
+    assert declared_functions() == sorted(_capi.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_capi.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    for sym in declared_functions():
+        assert sym in exported, sym
+        getattr(lib, sym)
+
+
+def test_abi_version(lib):
+    assert lib.mimir_prefixlm_abi_version() == _capi.ABI_VERSION
+
+
+def test_workspace_bytes(lib):
+    assert lib.mimir_prefixlm_bwd_workspace_bytes(16384, 16) == 16384 * 16 * 4
+    assert lib.mimir_prefixlm_bwd_workspace_bytes(0, 16) == 0
+
+
+def _c_layout(struct_name, fields):
+    """offsetof / sizeof of a header struct, from a C program built with gcc."""
+    src = '#include <stdio.h>\n#include <stddef.h>\n#include "mimir_prefixlm.h"\nint main(void){\n'
+    src += f'printf("%zu\\n", sizeof({struct_name}));\n'
+    for f in fields:
+        src += f'printf("%zu\\n", offsetof({struct_name}, {f}));\n'
+    src += "return 0;}\n"
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "layout.c")
+        exe = os.path.join(d, "layout")
+        with open(c, "w") as fh:
+            fh.write(src)
+        subprocess.run(["gcc", "-I", str(HEADER.parent), c, "-o", exe], check=True)
+        vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    return vals[0], vals[1:]
+
+
+@pytest.mark.parametrize("cls,name", [(_capi.FwdParams, "MimirPrefixLMFwdParams"),
+                                      (_capi.BwdParams, "MimirPrefixLMBwdParams")])
+def test_ctypes_struct_matches_c_layout(cls, name):
+    fields = [f for f, _ in cls._fields_]
+    size, offsets = _c_layout(name, fields)
+    assert ctypes.sizeof(cls) == size
+    assert [getattr(cls, f).offset for f in fields] == offsets
+
+
+def test_null_params_is_invalid_argument(lib):
+    assert lib.mimir_prefixlm_fwd(None, None) == _capi.ERR_INVALID_ARGUMENT
+    assert b"NULL" in lib.mimir_prefixlm_last_error()
+    assert lib.mimir_prefixlm_bwd(None, None) == _capi.ERR_INVALID_ARGUMENT
+
+
+def _fwd(**kw):
+    p = _capi.FwdParams()
+    base = dict(total_tokens=16, num_q_heads=4, num_kv_heads=2, head_dim=128, numseqs=1, total_seqlen=16,
+                max_seqlen_all=16, dtype=_capi.DTYPE_BFLOAT16, softmax_scale=0.088)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_validation_errors_map_to_reference_exceptions(lib):
+    rc = lib.mimir_prefixlm_fwd(ctypes.byref(_fwd(num_q_heads=3)), None)
+    assert rc == _capi.ERR_INVALID_ARGUMENT
+    assert b"Query heads 3 must be divisible by key/value heads 2." in lib.mimir_prefixlm_last_error()
+    with pytest.raises(ValueError, match="divisible"):
+        _capi.raise_for_status(lib, rc)
+
+    rc = lib.mimir_prefixlm_fwd(ctypes.byref(_fwd(dtype=7)), None)
+    assert rc == _capi.ERR_UNSUPPORTED_DTYPE
+    with pytest.raises(TypeError):
+        _capi.raise_for_status(lib, rc)
+
+    rc = lib.mimir_prefixlm_fwd(ctypes.byref(_fwd(head_dim=96)), None)
+    assert rc == _capi.ERR_UNSUPPORTED_SHAPE
+    assert b"head_dim 96" in lib.mimir_prefixlm_last_error()
+
+    rc = lib.mimir_prefixlm_fwd(ctypes.byref(_fwd(total_seqlen=17)), None)
+    assert rc == _capi.ERR_INVALID_ARGUMENT
+
+    rc = lib.mimir_prefixlm_fwd(ctypes.byref(_fwd(softmax_scale=0.0)), None)
+    assert rc == _capi.ERR_INVALID_ARGUMENT
+
+    # q is NULL: rejected before any launch
+    rc = lib.mimir_prefixlm_fwd(ctypes.byref(_fwd()), None)
+    assert rc == _capi.ERR_INVALID_ARGUMENT and b"q is NULL" in lib.mimir_prefixlm_last_error()
+
+
+def test_unknown_backward_stage_bits(lib):
+    p = _capi.BwdParams()
+    assert lib.mimir_prefixlm_bwd_stages(ctypes.byref(p), 64, None) == _capi.ERR_INVALID_ARGUMENT
+
+
+def test_last_error_is_thread_local(lib):
+    import threading
+
+    lib.mimir_prefixlm_fwd(None, None)
+    seen = []
+
+    def worker():
+        seen.append(lib.mimir_prefixlm_last_error())
+
+    t = threading.Thread(target=worker)
+    t.start()
+    t.join()
+    assert seen == [b""]
+    assert lib.mimir_prefixlm_last_error() != b""
