@@ -46,8 +46,16 @@ def _cores() -> int:
     return max(1, n)
 
 
-def cpu_baseline(case, seconds_cap: float = 30.0) -> dict:
-    """Oracle masked-SDPA fwd+bwd (fp32) on the first sequence of the batch."""
+def cpu_baseline(case, target_seconds: float = 12.0, unit_bytes_cap: float = 3e9) -> dict:
+    """Oracle masked-SDPA fwd+bwd (fp32, autograd) over a bounded sample of the batch.
+
+    The sample is a round-robin over units = (sequence, range of q-heads), each
+    run densely as its own packed batch, until about ``target_seconds`` of CPU
+    time have been spent (after one untimed warm-up unit).  A unit holds as many
+    whole kv-head groups as fit in ``unit_bytes_cap`` of fp32 score matrices, or
+    fewer q-heads of one group when a single group does not fit.  FLOPs count
+    the unit's attended pairs only, like the GPU figure.
+    """
     import torch
 
     from oracle.prefixlm_oracle import dense_forward_autograd
@@ -55,45 +63,81 @@ def cpu_baseline(case, seconds_cap: float = 30.0) -> dict:
 
     cores = _cores()
     torch.set_num_threads(cores)
-    n, p = case.seq_lens[0], case.prefixes[0]
-    s0 = int(case.cu_seqlens[0])
-    sl = slice(s0, s0 + n)
-    tens = tuple(t[sl].float().contiguous() for t in (case.q, case.k, case.v, case.dout))
-    sample = build_case(tens, [n], [p], is_causal=case.is_causal)
-    flops = sample.fwd_flops() + sample.bwd_flops()
+    hq, hkv = case.q.shape[1], case.k.shape[1]
+    group = hq // hkv
+    units = []   # (sequence, first q-head, q-heads, first kv head, kv heads)
+    for si, n in enumerate(case.seq_lens):
+        fit = max(1, int(unit_bytes_cap // (6.0 * 4.0 * n * n)))   # scores, probabilities, their grads
+        if fit >= group:
+            kv_w = max(d_ for d_ in range(1, hkv + 1) if hkv % d_ == 0 and d_ * group <= fit)
+            units += [(si, kv0 * group, kv_w * group, kv0, kv_w) for kv0 in range(0, hkv, kv_w)]
+        else:
+            w = max(d_ for d_ in range(1, group + 1) if group % d_ == 0 and d_ <= fit)
+            units += [(si, q0, w, q0 // group, 1) for q0 in range(0, hq, w)]
 
-    def run():
-        q, k, v = (t.clone().requires_grad_(True) for t in sample_tensors)
+    def make(unit):
+        si, q0, qw, kv0, kvw = unit
+        n, p = case.seq_lens[si], case.prefixes[si]
+        s0 = int(case.cu_seqlens[si])
+        sl = slice(s0, s0 + n)
+        tens = (case.q[sl, q0:q0 + qw].float().contiguous(), case.k[sl, kv0:kv0 + kvw].float().contiguous(),
+                case.v[sl, kv0:kv0 + kvw].float().contiguous(), case.dout[sl, q0:q0 + qw].float().contiguous())
+        return build_case(tens, [n], [p], is_causal=case.is_causal)
+
+    def run(sample):
+        q, k, v = (t.clone().requires_grad_(True) for t in (sample.q, sample.k, sample.v))
         o = dense_forward_autograd(q, k, v, sample.is_causal, *sample.oracle_args())
         o.backward(sample.dout)
 
-    sample_tensors = (sample.q, sample.k, sample.v)
-    t0 = time.perf_counter()
-    run()  # warm-up
-    first = time.perf_counter() - t0
-    reps = max(1, min(3, int(seconds_cap / max(first, 1e-3))))
-    times = []
-    for _ in range(reps):
+    run(make(units[0]))  # warm-up
+    flops = 0.0
+    elapsed = 0.0
+    done = 0
+    while elapsed < target_seconds:
+        sample = make(units[done % len(units)])
         t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
+        run(sample)
+        elapsed += time.perf_counter() - t0
+        flops += sample.fwd_flops() + sample.bwd_flops()
+        done += 1
     try:
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except Exception:  # noqa: BLE001
         model = "unknown"
+    widths = sorted({u[2] for u in units})
     return {
-        "value": round(flops / sec / 1e12, 5),
+        "value": round(flops / elapsed / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"fwd+bwd of sequence 0 (n={n}, prefix={p}, Hq={case.q.shape[1]}, Hkv={case.k.shape[1]}, "
-                   f"D={case.q.shape[2]}) of the same batch, fp32 torch SDPA with bool mask + autograd, "
-                   f"median of {reps} after 1 warm-up"),
-        "seconds": round(sec, 4),
+        "sample": (f"{done} units of (sequence, {'/'.join(map(str, widths))} q-heads) of the "
+                   f"same batch ({len(units)} units cover it; round-robin from sequence 0), each fwd+bwd as fp32 "
+                   f"torch SDPA with a bool prefix-LM mask + autograd; {elapsed:.1f} s timed after 1 warm-up unit"),
+        "seconds": round(elapsed, 3),
         "cpu_model": model,
         "torch": torch.__version__,
     }
+
+
+def _measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of ``kernel`` on ``workload`` from the committed PMC summary.
+
+    profiles/hbm_traffic.json holds FETCH_SIZE and WRITE_SIZE per dispatch from two
+    rocprofv3 --pmc runs of this script, each scaled by what the same counter reads
+    for a plain 1 GiB device copy; None when the workload was not profiled.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as fh:
+            data = json.load(fh)
+        entry = data["workloads"][workload][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    cal = data["calibration"]
+    return {"bytes": int(entry["bytes"]),
+            "source": (f"profiles/hbm_traffic.json (tree {data.get('commit', '?')}): FETCH_SIZE {entry['fetch_kib']} KiB x "
+                       f"{cal['fetch_factor']} + WRITE_SIZE {entry['write_kib']} KiB x {cal['write_factor']}, factors "
+                       f"from a 1 GiB device copy")}
 
 
 def copy_calibration(torch, dev, mib: int, reps: int) -> int:
@@ -249,6 +293,10 @@ def main() -> int:
             "algorithmic_flops_per_launch": kernel_flops[dom],
         },
     }
+    measured = _measured_traffic(CONFIG_NAMES[args.workload], kernel_names[dom])
+    if measured is not None:
+        res["roofline"]["traffic"] = measured["bytes"]
+        res["roofline"]["traffic_source"] = measured["source"]
     if not fwd_only:
         bwd_ms = sum(stage_avg[n] for n in ("delta", "dkdv", "dq", "fill"))
         res["bwd_tflops"] = round(f_bwd / (bwd_ms * 1e-3) / 1e12, 2)

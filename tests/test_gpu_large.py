@@ -6,11 +6,15 @@ from the closed form restricted to those rows, all keys) plus size-independent
 invariants that hold for every workload.
 
 dQ of the long-context workload (one q/k channel scaled x20, near one-hot softmax
-rows) is compared with the closed form whose delta = rowsum(dO * O) uses the
-stored bf16 O, the operand every bf16 backward receives (the reference's FA4
-wrapper included). Against the all-fp32 closed form the bf16 rounding of O alone
-moves dQ by about 0.4 on these rows, so that comparison is reported and bounded
-by twice that intrinsic shift instead of by 5e-2.
+rows) is compared with the closed form evaluated on the operands a flash backward
+receives and multiplies: the saved lse and bf16 O (delta = rowsum(dO * O)), and dS
+rounded to bf16 before the dS K product (the reference's FA4 wrapper does the
+same). Near one-hot rows amplify a 2e-4 lse difference, which fp32 accumulation
+of |S| ~ 300 logits can leave, into ~0.2 of dQ on the x20 channel, so the saved
+lse is the operand to compare against. On these
+rows those two roundings alone move dQ by 0.44 from the all-fp32 closed form
+(0.40 from O, 0.19 from dS), so the all-fp32 comparison is reported and bounded by
+1.5 x that emulated shift plus 5e-2, while the operand-matched comparison keeps 5e-2.
 
 Invariants:
 
@@ -96,8 +100,11 @@ def test_long_context_sampled_rows(device):
         dp = dof[:, h] @ vf[:, h].T
         o_stored = out[rows, h].float().cpu()
         dq_fp32 = (pr * (dp - (dof[:, h] * o).sum(1, keepdim=True)) * scale) @ kf[:, h]
-        dq_bf16o = (pr * (dp - (dof[:, h] * o_stored).sum(1, keepdim=True)) * scale) @ kf[:, h]
-        dq_ref_o = (pr * (dp - (dof[:, h] * o.bfloat16().float()).sum(1, keepdim=True)) * scale) @ kf[:, h]
+        pr_saved = torch.exp(s - lse[h, rows].cpu()[:, None])
+        ds = pr_saved * (dp - (dof[:, h] * o_stored).sum(1, keepdim=True))
+        dq_bf16o = (ds.bfloat16().float() @ kf[:, h]) * scale
+        ds_ref = pr * (dp - (dof[:, h] * o.bfloat16().float()).sum(1, keepdim=True))
+        dq_ref_o = (ds_ref.bfloat16().float() @ kf[:, h]) * scale
         got = dq[rows, h].float().cpu()
         worst["o"] = max(worst["o"], (o_stored - o).abs().max().item())
         worst["lse"] = max(worst["lse"], (lse[h, rows].cpu() - ref_lse).abs().max().item())
@@ -106,7 +113,7 @@ def test_long_context_sampled_rows(device):
         worst["intrinsic"] = max(worst.get("intrinsic", 0.0), (dq_ref_o - dq_fp32).abs().max().item())
     print(f"[cfg4 sampled rows] {worst} rows={rows.numel()}", flush=True)
     assert worst["o"] <= 2e-2 and worst["lse"] <= 1e-2 and worst["dq"] <= 5e-2, worst
-    assert worst["dq_vs_fp32"] <= 2 * worst["intrinsic"] + 5e-2, worst
+    assert worst["dq_vs_fp32"] <= 1.5 * worst["intrinsic"] + 5e-2, worst
     # the sampled mask agrees with the reference mask statement
     assert torch.equal(prefixlm_mask(n, p, False)[rows[:4]], (torch.arange(n)[None, :] <
                                                              torch.clamp(rows[:4, None] + 1, min=p)))

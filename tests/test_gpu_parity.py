@@ -88,6 +88,7 @@ SMALL = [
     ([300], [100], 2, 2, 64, None, False),
     ([512, 200, 1, 77], [0, 200, 1, 30], 8, 2, 64, 1000, False),
     ([1000, 24], [500, 0], 8, 8, 64, None, False),
+    ([190, 64, 3], [64, 64, 0], 16, 2, 128, 300, False),
 ]
 
 
@@ -99,7 +100,7 @@ def test_bf16_small(device, idx):
     check(case, device, label=f"small{idx}")
 
 
-@pytest.mark.parametrize("idx", [0, 1, 2, 4, 5, 6])
+@pytest.mark.parametrize("idx", [0, 1, 2, 4, 5, 6, 8])
 def test_f32_small(device, idx):
     seq_lens, prefixes, hq, hkv, d, pad_to, causal = SMALL[idx]
     case = make_case(seq_lens, prefixes, hq, hkv, d, seed=100 + idx, dtype=torch.float32, pad_to=pad_to,
@@ -140,3 +141,13 @@ def test_deterministic(device):
     b = run_gpu(case, device)
     for key in a:
         assert torch.equal(a[key], b[key]), key
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_empty_batch_is_all_padding(device, dtype):
+    """numseqs = 0: every row is padding (O = 0, lse = -inf, zero gradients), nothing else launched."""
+    case = make_case([], [], 4, 2, 64, seed=5, dtype=dtype, pad_to=40)
+    got = run_gpu(case, device)
+    assert torch.count_nonzero(got["o"]) == 0 and torch.isneginf(got["lse"]).all()
+    for key in ("dq", "dk", "dv"):
+        assert torch.count_nonzero(got[key]) == 0, key
