@@ -141,7 +141,7 @@ int mimir_prefixlm_bwd(const MimirPrefixLMBwdParams* params, void* stream);
  * independent of each other.  No reference counterpart: the reference exposes
  * the backward only through autograd (flash_attention_prefixlm_v2.py:270-283). */
 enum MimirBwdStage {
-  MIMIR_BWD_STAGE_DELTA = 1, /* delta = rowsum(O * dO) into the workspace */
+  MIMIR_BWD_STAGE_DELTA = 1, /* delta = rowsum(O * dO) and lse * log2(e) into the workspace */
   MIMIR_BWD_STAGE_DKDV = 2,  /* dK, dV for every key row inside a sequence */
   MIMIR_BWD_STAGE_DQ = 4,    /* dQ for every active query row */
   MIMIR_BWD_STAGE_FILL = 8,  /* zero dQ / dK / dV rows outside every sequence */
@@ -149,7 +149,8 @@ enum MimirBwdStage {
 };
 int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* params, int stages, void* stream);
 
-/* Bytes of device workspace the backward needs (float32 delta [Hq, T]). */
+/* Bytes of device workspace the backward needs: float32 delta = rowsum(O * dO) [Hq, T]
+ * and float32 lse * log2(e) [Hq, T], both written by the DELTA stage. */
 size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads);
 
 /* Device-side metadata check: writes to *bad_seq (device int32) the first s in

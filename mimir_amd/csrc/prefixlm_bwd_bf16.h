@@ -19,7 +19,8 @@ struct BwdArgs {
   bf16_t* dq;
   bf16_t* dk;
   bf16_t* dv;
-  float* delta;
+  float* delta;      // workspace [Hq, T]: rowsum(dO * O)
+  float* lse2;       // workspace [Hq, T]: lse * log2(e), the exp2-domain row offset
   const int32_t* prefix_lens;
   const int32_t* cu_seqlens;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, do_st, do_sh;

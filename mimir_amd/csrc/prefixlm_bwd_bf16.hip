@@ -28,7 +28,9 @@ namespace {
 using namespace mimir;
 
 // ---------------------------------------------------------------------------
-// delta = rowsum(O * dO), one (token, head) row per D/8 lanes.
+// delta = rowsum(O * dO), one (token, head) row per D/8 lanes; the same pass
+// stores lse * log2(e), so the tile loops form P = exp2(S * scale * log2(e) - lse2)
+// with one FMA per score.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void delta_kernel(const BwdArgs a) {
@@ -48,7 +50,10 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdArgs a) {
   }
 #pragma unroll
   for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (valid && c == 0) a.delta[(int64_t)h * a.T + t] = acc;
+  if (valid && c == 0) {
+    a.delta[(int64_t)h * a.T + t] = acc;
+    a.lse2[(int64_t)h * a.T + t] = a.lse[(int64_t)h * a.lse_sh + t] * kLog2e;
+  }
 }
 
 template <int D>
@@ -64,6 +69,7 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stage
   a.dk = (bf16_t*)p.dk;
   a.dv = (bf16_t*)p.dv;
   a.delta = (float*)p.workspace;
+  a.lse2 = (float*)p.workspace + (int64_t)p.num_q_heads * p.total_tokens;
   a.prefix_lens = p.prefix_lens;
   a.cu_seqlens = p.cu_seqlens;
   a.q_st = p.q_stride_token; a.q_sh = p.q_stride_head;

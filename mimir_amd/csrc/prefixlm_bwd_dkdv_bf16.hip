@@ -84,7 +84,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
     ldq.issue(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, qb, g.nq, tq);
     ldo.issue(a.dout + (int64_t)g.start * a.do_st + (int64_t)h * a.do_sh, qb, g.nq, to);
     if (wave == 0) {
-      const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse + (int64_t)h * a.lse_sh + g.start, (uint32_t)g.nq * 4u);
+      const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse2 + (int64_t)h * a.T + g.start, (uint32_t)g.nq * 4u);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (__attribute__((address_space(3))) void*)tl, 4,
                                                (uint32_t)(qb + lane) * 4u, 0, 0, 0);
     } else {
@@ -116,11 +116,12 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   const float c2 = a.scale_log2;
   const TileLanes<D> tl(lane);
 
-  auto compute = [&](int it, const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
-    const int hh = it / nqt;
-    const int qb = q_begin + (it - hh * nqt) * kBwdBlockQT;
-    if (!wave_active || qb + kBwdBlockQT <= w_qs_min) return;
-    const bool masked = (qb < w_qs_max) || (qb + kBwdBlockQT > g.nq);
+  // One (q head, 64-query tile) step.  Masked tiles (queries before some key's
+  // qstart, or past the sequence end) overwrite the disallowed scores with -inf
+  // in one guarded pass right after the S MFMAs; the softmax and the dV / dK
+  // MFMAs that follow are one straight-line block for both kinds of tile.
+  auto compute = [&](bool masked, int qb, const bf16_t* sQ, const bf16_t* sdO, const float* sL,
+                     const float* sD) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {  // 32-query halves of the tile
       f32x16 sc[NS], dp[NS];
@@ -141,6 +142,20 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
         }
       }
       // rows of sc / dp: query 32*mt + 8*(r/4) + 4*hi + r%4 ; column: the lane's key.
+      if (masked) {
+        // allowed iff qs_lane <= q < nq, i.e. (unsigned)(q - qs_lane) < (unsigned)(nq - qs_lane).
+        // The empty volatile asm keeps this block a real branch: if-converted, its
+        // 48 VALU operations would run on every unmasked tile as well.
+        __asm__ volatile("");
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+          const unsigned base = (unsigned)(qb + 32 * mt + 4 * hi - qs_lane[j]);
+          const unsigned lim = (unsigned)(g.nq - qs_lane[j]);
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (base + (unsigned)(8 * (r >> 2) + (r & 3)) >= lim) sc[j][r] = -INFINITY;
+        }
+      }
       // Each 16-query half (s2) is converted to bf16 right before its MFMAs so
       // that its fp32 scores die early.
 #pragma unroll
@@ -158,11 +173,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int r = 4 * rg + e;
-              float pr = fast_exp2(__builtin_fmaf(sc[j][r], c2, -l4[e] * kLog2e));
-              if (masked) {
-                const int qp = qb + qr0 + e;
-                if (qp < qs_lane[j] || qp >= g.nq) pr = 0.f;
-              }
+              const float pr = fast_exp2(__builtin_fmaf(sc[j][r], c2, -l4[e]));
               tp[4 * rg2 + e] = pr;
               tds[4 * rg2 + e] = pr * (dp[j][r] - d4[e]);
             }
@@ -185,17 +196,23 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
       }
     }
   };
+  auto step = [&](int it, const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
+    const int hh = it / nqt;
+    const int qb = q_begin + (it - hh * nqt) * kBwdBlockQT;
+    if (!wave_active || qb + kBwdBlockQT <= w_qs_min) return;
+    compute((qb < w_qs_max) || (qb + kBwdBlockQT > g.nq), qb, sQ, sdO, sL, sD);
+  };
 
   for (int it = 0; it < n_iter; it += 2) {
     wait_vmem();
     __syncthreads();
     if (it + 1 < n_iter) issue(it + 1, sQ1, sO1, sL1, sD1);
-    compute(it, sQ0, sO0, sL0, sD0);
+    step(it, sQ0, sO0, sL0, sD0);
     if (it + 1 >= n_iter) break;
     wait_vmem();
     __syncthreads();
     if (it + 2 < n_iter) issue(it + 2, sQ0, sO0, sL0, sD0);
-    compute(it + 1, sQ1, sO1, sL1, sD1);
+    step(it + 1, sQ1, sO1, sL1, sD1);
   }
 
   if (!wave_active) return;

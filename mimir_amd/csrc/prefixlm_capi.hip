@@ -146,7 +146,8 @@ int mimir_prefixlm_abi_version(void) { return MIMIR_PREFIXLM_ABI_VERSION; }
 
 size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads) {
   if (total_tokens <= 0 || num_q_heads <= 0) return 0;
-  return (size_t)total_tokens * (size_t)num_q_heads * sizeof(float);
+  // float32 delta [Hq, T] followed by float32 lse * log2(e) [Hq, T]
+  return 2 * (size_t)total_tokens * (size_t)num_q_heads * sizeof(float);
 }
 
 int mimir_prefixlm_check_metadata(const int32_t* prefix_lens, const int32_t* causal_lens,

@@ -21,6 +21,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Compile-time flag for generic lambdas (masked / unmasked tile bodies).
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 

@@ -50,7 +50,7 @@ def test_abi_version(lib):
 
 
 def test_workspace_bytes(lib):
-    assert lib.mimir_prefixlm_bwd_workspace_bytes(16384, 16) == 16384 * 16 * 4
+    assert lib.mimir_prefixlm_bwd_workspace_bytes(16384, 16) == 2 * 16384 * 16 * 4
     assert lib.mimir_prefixlm_bwd_workspace_bytes(0, 16) == 0
 
 
