@@ -99,14 +99,24 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
         dpt[mt] = mfma32(vf, dof[ks], dpt[mt]);
       }
     }
-    const bool masked = kb + kBlockK > w_kend_min;
+    if (kb + kBlockK > w_kend_min) {
+      // Tile reaches past some row's kend: disallowed scores become -inf (P = 0).
+      // The empty volatile asm keeps this a real branch, so unmasked tiles do not
+      // pay for the compares.
+      __asm__ volatile("");
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kpos = kb + 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
+          if (kpos >= kend_lane) st[mt][r] = -INFINITY;
+        }
+    }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kpos = kb + 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
-        float pr = fast_exp2(__builtin_fmaf(st[mt][r], c2, -lse2));
-        if (masked && kpos >= kend_lane) pr = 0.f;
+        const float pr = fast_exp2(__builtin_fmaf(st[mt][r], c2, -lse2));
         st[mt][r] = pr * (dpt[mt][r] - dlt);
       }
     bf16x8 sf[4];
