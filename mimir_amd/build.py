@@ -34,6 +34,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# Per-source code generation options (none at present).
+SOURCE_FLAGS: dict = {}
+
 SOURCES = [
     "prefixlm_capi.hip",
     "prefixlm_fwd_bf16.hip",
@@ -56,7 +59,7 @@ def hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)

@@ -6,25 +6,21 @@ namespace mimir {
 namespace {
 
 // ---------------------------------------------------------------------------
-// dK / dV.  Each wave owns kDkSub x 32 keys whose K and V fragments stay in
-// registers as B operands; lanes own key columns, so P and dS feed the B operand
-// of dV^T += dO^T P and dK^T += Q^T dS directly, and the transposed dO^T / Q^T
-// fragments come from the row-major LDS tiles via ds_read_b64_tr_b16.  Every Q /
-// dO operand read from LDS (plain or transposed) feeds kSub MFMAs, one per
-// 32-key subtile of the wave.
+// dK / dV.  Each wave owns 32 keys whose K and V fragments stay in registers as
+// B operands; lanes own key columns, so P and dS feed the B operand of
+// dV^T += dO^T P and dK^T += Q^T dS directly, and the transposed dO^T / Q^T
+// fragments come from the row-major LDS tiles via ds_read_b64_tr_b16.
 // The query range starts at qstart(first key) = (key < p ? 0 : key).
 // Grid: x = sequence * Hkv + kv head, y = key tile (prefix keys, the heaviest, first).
 //
-// Configuration per head_dim: one 32-key subtile per wave and four waves per
-// workgroup measured fastest for both 64 and 128 (two subtiles per wave halve
-// the LDS traffic per MFMA but exceed the register file at 128 and spill).
-// At 128 the K / V fragments and dK / dV accumulators need one wave per SIMD.
+// At head_dim 128 the K / V fragments and the dK / dV accumulators allow one
+// wave per SIMD, so LDS latency is hidden inside the wave: every operand
+// fragment is read one phase ahead (see compute below).
 // ---------------------------------------------------------------------------
 template <int D>
 struct DkCfg {
-  static constexpr int kSub = 1;                      // 32-key subtiles per wave
-  static constexpr int kWaves = 4;                    // waves per workgroup
-  static constexpr int kKeys = 32 * kSub * kWaves;    // keys per workgroup
+  static constexpr int kWaves = 4;                    // waves per workgroup, 32 keys each
+  static constexpr int kKeys = 32 * kWaves;           // keys per workgroup
   static constexpr int kWavesPerSimd = D <= 64 ? 2 : 1;
 };
 
@@ -32,7 +28,6 @@ template <int D>
 __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) void dkdv_kernel(const BwdArgs a) {
   constexpr int DT = D / 32;
   constexpr int KS = D / 16;
-  constexpr int NS = DkCfg<D>::kSub;
   constexpr int kDkWaves = DkCfg<D>::kWaves;
   constexpr int kDkKeys = DkCfg<D>::kKeys;
   using L = TileLayout<D>;
@@ -45,6 +40,10 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   __shared__ __attribute__((aligned(16))) float sD0[kBwdBlockQT];
   __shared__ __attribute__((aligned(16))) float sL1[kBwdBlockQT];
   __shared__ __attribute__((aligned(16))) float sD1[kBwdBlockQT];
+  __shared__ __attribute__((aligned(16))) bf16_t sQ2[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sO2[L::kElems];
+  __shared__ __attribute__((aligned(16))) float sL2[kBwdBlockQT];
+  __shared__ __attribute__((aligned(16))) float sD2[kBwdBlockQT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -59,13 +58,11 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   const int kb0 = ktile * kDkKeys;
   if (kb0 >= g.n) return;
 
-  const int ka = kb0 + wave * 32 * NS;       // this wave's first key
+  const int ka = kb0 + wave * 32;            // this wave's first key
   const bool wave_active = ka < g.n;
-  int qs_lane[NS];                           // first query attending this lane's key of subtile j
-#pragma unroll
-  for (int j = 0; j < NS; ++j) qs_lane[j] = qstart_of(g.p, ka + 32 * j + l32);
+  const int qs_lane = qstart_of(g.p, ka + l32);  // first query attending this lane's key
   const int w_qs_min = qstart_of(g.p, ka);
-  const int w_qs_max = qstart_of(g.p, ka + 32 * NS - 1);
+  const int w_qs_max = qstart_of(g.p, ka + 31);
   const int q_begin = qstart_of(g.p, kb0);
   const int nqt = g.nq > q_begin ? (g.nq - q_begin + kBwdBlockQT - 1) / kBwdBlockQT : 0;
   const int n_iter = nqt * a.group;  // (q head, query tile) pairs
@@ -93,108 +90,123 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
                                                (uint32_t)(qb + lane) * 4u, 0, 0, 0);
     }
   };
+  // Three LDS stages: iteration it computes on stage it % 3 while the tiles of
+  // it + 1 and it + 2 are in flight.
   if (n_iter > 0) issue(0, sQ0, sO0, sL0, sD0);
 
-  bf16x8 kf[NS][KS], vf[NS][KS];
+  bf16x8 kf[KS], vf[KS];
 #pragma unroll
-  for (int j = 0; j < NS; ++j)
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int64_t key = ka + 32 * j + l32;
-      kf[j][ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
-      vf[j][ks] = __builtin_bit_cast(bf16x8, buf_load16(rv, (uint32_t)((key * a.v_st + 16 * ks + 8 * hi) * 2)));
-    }
+  for (int ks = 0; ks < KS; ++ks) {
+    const int64_t key = ka + l32;
+    kf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
+    vf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rv, (uint32_t)((key * a.v_st + 16 * ks + 8 * hi) * 2)));
+  }
+  if (n_iter > 1) issue(1, sQ1, sO1, sL1, sD1);
+  // Buffer loads per issue() and wave: Q and dO tiles plus one lse2 / delta row.
+  constexpr int kLoadsPerIssue = 2 * TileLoader<D, kDkWaves>::kPerWave + 1;
+  auto wait_stage = [&](int it) {  // tile `it` has landed; tile it + 1 may still be in flight
+    if (it + 1 < n_iter)
+      wait_vmcnt<kLoadsPerIssue>();
+    else
+      wait_vmem();
+  };
 
-  f32x16 dkacc[NS][DT], dvacc[NS][DT];
+  f32x16 dkacc[DT], dvacc[DT];
 #pragma unroll
-  for (int j = 0; j < NS; ++j)
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      dkacc[j][dt] = f32x16{};
-      dvacc[j][dt] = f32x16{};
-    }
+  for (int dt = 0; dt < DT; ++dt) {
+    dkacc[dt] = f32x16{};
+    dvacc[dt] = f32x16{};
+  }
   const float c2 = a.scale_log2;
   const TileLanes<D> tl(lane);
 
-  // One (q head, 64-query tile) step.  Masked tiles (queries before some key's
-  // qstart, or past the sequence end) overwrite the disallowed scores with -inf
-  // in one guarded pass right after the S MFMAs; the softmax and the dV / dK
-  // MFMAs that follow are one straight-line block for both kinds of tile.
+  // One (q head, 64-query tile) step, per 32-query half h:
+  //   S/dP MFMAs(h)      while the dO^T / Q^T fragments of h are read
+  //   softmax(h)         (VALU)
+  //   dV/dK MFMAs(h)     while the Q / dO fragments of h+1 are read
+  // so every LDS fragment is read one phase before the MFMAs that use it.
+  // Masked tiles (queries before some key's qstart, or past the sequence end)
+  // overwrite the disallowed scores with -inf in one guarded pass right after
+  // the S MFMAs.
   auto compute = [&](bool masked, int qb, const bf16_t* sQ, const bf16_t* sdO, const float* sL,
                      const float* sD) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {  // 32-query halves of the tile
-      f32x16 sc[NS], dp[NS];
-#pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        sc[j] = f32x16{};
-        dp[j] = f32x16{};
-      }
+    bf16x8 qa[KS], da[KS];          // Q / dO rows of one half: A operands of S / dP
+    bf16x8 ot[2][DT], qt[2][DT];    // dO^T / Q^T of one half: A operands of dV^T / dK^T
+    auto load_s = [&](int mt) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const int o = tl.op_base + mt * 32 * L::kRowElems + ks * 16;
-        const bf16x8 qa8 = *(const bf16x8*)&sQ[o];
-        const bf16x8 da8 = *(const bf16x8*)&sdO[o];
-#pragma unroll
-        for (int j = 0; j < NS; ++j) {
-          sc[j] = mfma32(qa8, kf[j][ks], sc[j]);
-          dp[j] = mfma32(da8, vf[j][ks], dp[j]);
-        }
+        qa[ks] = *(const bf16x8*)&sQ[o];
+        da[ks] = *(const bf16x8*)&sdO[o];
       }
+    };
+    auto load_t = [&](int mt) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int o = tl.tr_base + (2 * mt + s2) * 16 * L::kRowElems + dt * 32;
+          ot[s2][dt] = cat8(lds_read_tr16(&sdO[o]), lds_read_tr16(&sdO[o + L::kTrSecond]));
+          qt[s2][dt] = cat8(lds_read_tr16(&sQ[o]), lds_read_tr16(&sQ[o + L::kTrSecond]));
+        }
+    };
+
+    load_s(0);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {  // 32-query halves of the tile
+      f32x16 sc = f32x16{}, dp = f32x16{};
+      __builtin_amdgcn_sched_barrier(0);
+      load_t(mt);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        sc = mfma32(qa[ks], kf[ks], sc);
+        dp = mfma32(da[ks], vf[ks], dp);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       // rows of sc / dp: query 32*mt + 8*(r/4) + 4*hi + r%4 ; column: the lane's key.
       if (masked) {
         // allowed iff qs_lane <= q < nq, i.e. (unsigned)(q - qs_lane) < (unsigned)(nq - qs_lane).
         // The empty volatile asm keeps this block a real branch: if-converted, its
         // 48 VALU operations would run on every unmasked tile as well.
         __asm__ volatile("");
+        const unsigned base = (unsigned)(qb + 32 * mt + 4 * hi - qs_lane);
+        const unsigned lim = (unsigned)(g.nq - qs_lane);
 #pragma unroll
-        for (int j = 0; j < NS; ++j) {
-          const unsigned base = (unsigned)(qb + 32 * mt + 4 * hi - qs_lane[j]);
-          const unsigned lim = (unsigned)(g.nq - qs_lane[j]);
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (base + (unsigned)(8 * (r >> 2) + (r & 3)) >= lim) sc[j][r] = -INFINITY;
-        }
+        for (int r = 0; r < 16; ++r)
+          if (base + (unsigned)(8 * (r >> 2) + (r & 3)) >= lim) sc[r] = -INFINITY;
       }
-      // Each 16-query half (s2) is converted to bf16 right before its MFMAs so
-      // that its fp32 scores die early.
+      bf16x8 pb[2], db[2];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        bf16x8 pb[NS], db[NS];
+        f32x8 tp, tds;
 #pragma unroll
-        for (int j = 0; j < NS; ++j) {
-          f32x8 tp, tds;
+        for (int rg2 = 0; rg2 < 2; ++rg2) {
+          const int rg = 2 * s2 + rg2;
+          const int qr0 = 32 * mt + 8 * rg + 4 * hi;
+          const f32x4 l4 = *(const f32x4*)&sL[qr0];
+          const f32x4 d4 = *(const f32x4*)&sD[qr0];
 #pragma unroll
-          for (int rg2 = 0; rg2 < 2; ++rg2) {
-            const int rg = 2 * s2 + rg2;
-            const int qr0 = 32 * mt + 8 * rg + 4 * hi;
-            const f32x4 l4 = *(const f32x4*)&sL[qr0];
-            const f32x4 d4 = *(const f32x4*)&sD[qr0];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int r = 4 * rg + e;
-              const float pr = fast_exp2(__builtin_fmaf(sc[j][r], c2, -l4[e]));
-              tp[4 * rg2 + e] = pr;
-              tds[4 * rg2 + e] = pr * (dp[j][r] - d4[e]);
-            }
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * rg + e;
+            const float pr = fast_exp2(__builtin_fmaf(sc[r], c2, -l4[e]));
+            tp[4 * rg2 + e] = pr;
+            tds[4 * rg2 + e] = pr * (dp[r] - d4[e]);
           }
-          pb[j] = to_bf16x8(tp);
-          db[j] = to_bf16x8(tds);
         }
-        const int kk = 2 * mt + s2;  // 16-query step inside the 64-row tile
+        pb[s2] = to_bf16x8(tp);
+        db[s2] = to_bf16x8(tds);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (mt == 0) load_s(1);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const int o = tl.tr_base + kk * 16 * L::kRowElems + dt * 32;
-          const bf16x8 ot = cat8(lds_read_tr16(&sdO[o]), lds_read_tr16(&sdO[o + L::kTrSecond]));
-          const bf16x8 qt = cat8(lds_read_tr16(&sQ[o]), lds_read_tr16(&sQ[o + L::kTrSecond]));
-#pragma unroll
-          for (int j = 0; j < NS; ++j) {
-            dvacc[j][dt] = mfma32(ot, pb[j], dvacc[j][dt]);
-            dkacc[j][dt] = mfma32(qt, db[j], dkacc[j][dt]);
-          }
+          dvacc[dt] = mfma32(ot[s2][dt], pb[s2], dvacc[dt]);
+          dkacc[dt] = mfma32(qt[s2][dt], db[s2], dkacc[dt]);
         }
-      }
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
   auto step = [&](int it, const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
     const int hh = it / nqt;
@@ -203,39 +215,43 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
     compute((qb < w_qs_max) || (qb + kBwdBlockQT > g.nq), qb, sQ, sdO, sL, sD);
   };
 
-  for (int it = 0; it < n_iter; it += 2) {
-    wait_vmem();
+  // After the barrier of iteration it every wave is done with iteration it - 1,
+  // whose stage ((it + 2) % 3) then receives tile it + 2.
+  for (int it = 0; it < n_iter; it += 3) {
+    wait_stage(it);
     __syncthreads();
-    if (it + 1 < n_iter) issue(it + 1, sQ1, sO1, sL1, sD1);
+    if (it + 2 < n_iter) issue(it + 2, sQ2, sO2, sL2, sD2);
     step(it, sQ0, sO0, sL0, sD0);
     if (it + 1 >= n_iter) break;
-    wait_vmem();
+    wait_stage(it + 1);
     __syncthreads();
-    if (it + 2 < n_iter) issue(it + 2, sQ0, sO0, sL0, sD0);
+    if (it + 3 < n_iter) issue(it + 3, sQ0, sO0, sL0, sD0);
     step(it + 1, sQ1, sO1, sL1, sD1);
+    if (it + 2 >= n_iter) break;
+    wait_stage(it + 2);
+    __syncthreads();
+    if (it + 4 < n_iter) issue(it + 4, sQ1, sO1, sL1, sD1);
+    step(it + 2, sQ2, sO2, sL2, sD2);
   }
 
   if (!wave_active) return;
+  const int kpos = ka + l32;
+  if (kpos >= g.n) return;
+  bf16_t* krow = a.dk + (int64_t)(g.start + kpos) * a.dk_st + (int64_t)hk * a.dk_sh;
+  bf16_t* vrow = a.dv + (int64_t)(g.start + kpos) * a.dv_st + (int64_t)hk * a.dv_sh;
 #pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    const int kpos = ka + 32 * j + l32;
-    if (kpos >= g.n) continue;
-    bf16_t* krow = a.dk + (int64_t)(g.start + kpos) * a.dk_st + (int64_t)hk * a.dk_sh;
-    bf16_t* vrow = a.dv + (int64_t)(g.start + kpos) * a.dv_st + (int64_t)hk * a.dv_sh;
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+    for (int rg = 0; rg < 4; ++rg) {
+      f32x4 tk, tv;
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        f32x4 tk, tv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          tk[e] = dkacc[j][dt][4 * rg + e] * a.scale;
-          tv[e] = dvacc[j][dt][4 * rg + e];
-        }
-        *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tk, bf16x4);
-        *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
+      for (int e = 0; e < 4; ++e) {
+        tk[e] = dkacc[dt][4 * rg + e] * a.scale;
+        tv[e] = dvacc[dt][4 * rg + e];
       }
-  }
+      *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tk, bf16x4);
+      *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
+    }
 }
 
 

@@ -234,6 +234,13 @@ struct TileLanes {
 
 // s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (they complete in issue order, so everything older than the last N is done).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate (low field)");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
 
 }  // namespace mimir
 
