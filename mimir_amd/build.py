@@ -43,6 +43,7 @@ SOURCES = [
     "prefixlm_bwd_bf16.hip",
     "prefixlm_bwd_dq_bf16.hip",
     "prefixlm_bwd_dkdv_bf16.hip",
+    "prefixlm_bwd_dkdv_pair_bf16.hip",
     "prefixlm_f32.hip",
 ]
 

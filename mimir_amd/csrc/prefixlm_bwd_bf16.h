@@ -43,5 +43,7 @@ struct BwdArgs {
 hipError_t launch_bwd_dq_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all, hipStream_t stream);
 hipError_t launch_bwd_dkdv_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all,
                                 hipStream_t stream);
+// head_dim 128, two waves per SIMD (prefixlm_bwd_dkdv_pair_bf16.hip)
+hipError_t launch_bwd_dkdv_pair_bf16(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream);
 
 }  // namespace mimir

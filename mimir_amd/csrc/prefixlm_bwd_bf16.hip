@@ -99,7 +99,8 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stage
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (stages & MIMIR_BWD_STAGE_DKDV) {
-    e = launch_bwd_dkdv_bf16(a, D, p.numseqs, p.max_seqlen_all, stream);
+    e = D == 128 ? launch_bwd_dkdv_pair_bf16(a, p.numseqs, p.max_seqlen_all, stream)
+                 : launch_bwd_dkdv_bf16(a, D, p.numseqs, p.max_seqlen_all, stream);
     if (e != hipSuccess) return e;
   }
   if (stages & MIMIR_BWD_STAGE_DQ) {

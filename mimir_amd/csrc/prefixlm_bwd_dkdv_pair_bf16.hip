@@ -1,0 +1,257 @@
+// bf16 prefix-LM attention backward, dK / dV kernel for head_dim 128 with two
+// waves per SIMD, for gfx950 (MI355X).  Owner = (kv head, 128-key tile), the
+// same split and grid as the one-wave-per-SIMD kernel in
+// prefixlm_bwd_dkdv_bf16.hip, and the same math:
+//   per q head of the GQA group and 64-query tile:
+//     S = Q K^T, dP = dO V^T, P = exp2(S * scale * log2 e - lse2),
+//     dS = P (dP - delta), dV^T += dO^T P, dK^T += Q^T dS.
+//
+// Workgroup = 8 waves.  Waves w and w + 4 own the same 32 keys (key slice
+// w % 4, both on SIMD w % 4) and take the two 32-query halves of every 64-query
+// tile (half w / 4), so each keeps its own dK / dV partial sums over half of the
+// queries; the pair's partials are added through LDS at the end.  To fit two
+// waves per SIMD (256 registers each) only the K fragments stay in registers:
+// the 128 x 128 V tile is staged in LDS once and read as the B operand of dP.
+// With two waves per SIMD the hardware overlaps one wave's softmax with the
+// other's MFMAs.
+#include "prefixlm_bwd_bf16.h"
+
+namespace mimir {
+namespace {
+
+constexpr int kPairWaves = 8;
+constexpr int kPairKeys = 128;
+constexpr int kPairD = 128;
+
+__global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const BwdArgs a) {
+  constexpr int D = kPairD;
+  constexpr int DT = D / 32;
+  constexpr int KS = D / 16;
+  using L = TileLayout<D>;
+  using Loader = TileLoader<D, kPairWaves>;
+  static_assert(kBwdBlockQT == 64, "one TileLayout tile per Q / dO block");
+
+  // LDS: three stages of (Q tile, dO tile, lse2 row, delta row), then the V tile
+  // (two 64-row TileLayout tiles).  After the tile loop the front of the same
+  // buffer holds the dK / dV partials of the second wave of each pair.
+  constexpr int kTileBytes = L::kElems * 2;
+  constexpr int kStageBytes = 2 * kTileBytes + 2 * kBwdBlockQT * 4;
+  constexpr int kVBytes = 2 * kTileBytes;
+  constexpr int kPartialBytes = 4 * 64 * 64 * 4;  // 4 slices x 64 floats x 64 lanes
+  constexpr int kLdsBytes = 3 * kStageBytes + kVBytes;
+  static_assert(kPartialBytes <= kLdsBytes, "partials reuse the stage buffers");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kLdsBytes];
+  auto stage_q = [&](int st) { return (bf16_t*)(smem + st * kStageBytes); };
+  auto stage_o = [&](int st) { return (bf16_t*)(smem + st * kStageBytes + kTileBytes); };
+  auto stage_l = [&](int st) { return (float*)(smem + st * kStageBytes + 2 * kTileBytes); };
+  auto stage_d = [&](int st) { return (float*)(smem + st * kStageBytes + 2 * kTileBytes + kBwdBlockQT * 4); };
+  bf16_t* const sV = (bf16_t*)(smem + 3 * kStageBytes);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slice = wave & 3;  // 32-key slice
+  const int qh = wave >> 2;    // 32-query half of each tile
+  const int l32 = lane & 31;
+  const int hi = lane >> 5;
+  if ((int)blockIdx.x >= a.grid_x) return;
+  const int hk = blockIdx.x % a.Hkv;
+  const int s = blockIdx.x / a.Hkv;
+  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const int kb0 = blockIdx.y * kPairKeys;
+  if (kb0 >= g.n) return;
+
+  const int ka = kb0 + slice * 32;  // first key of this wave's slice
+  const bool wave_active = ka < g.n;
+  const int qs_lane = qstart_of(g.p, ka + l32);
+  const int w_qs_min = qstart_of(g.p, ka);
+  const int w_qs_max = qstart_of(g.p, ka + 31);
+  const int q_begin = qstart_of(g.p, kb0);
+  const int nqt = g.nq > q_begin ? (g.nq - q_begin + kBwdBlockQT - 1) / kBwdBlockQT : 0;
+  const int n_iter = nqt * a.group;
+
+  const bf16_t* kseq = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
+  const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
+  const Loader ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane), ldv(a.v_st, wave, lane);
+  auto issue = [&](int it, int st) {
+    const int hh = it / nqt;
+    const int qb = q_begin + (it - hh * nqt) * kBwdBlockQT;
+    const int h = hk * a.group + hh;
+    ldq.issue(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, qb, g.nq, stage_q(st));
+    ldo.issue(a.dout + (int64_t)g.start * a.do_st + (int64_t)h * a.do_sh, qb, g.nq, stage_o(st));
+    // one 4-byte row load per wave: wave 0 lse2, the others delta (same data to the same place)
+    const bool lse_row = wave == 0;
+    const float* src = lse_row ? a.lse2 : a.delta;
+    float* dst = lse_row ? stage_l(st) : stage_d(st);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(src + (int64_t)h * a.T + g.start, (uint32_t)g.nq * 4u);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4,
+                                             (uint32_t)(qb + lane) * 4u, 0, 0, 0);
+  };
+
+  // V tile (keys kb0 .. kb0 + 127), then the first two Q / dO stages; the K
+  // fragments of this wave's slice go to registers.
+  ldv.issue(vseq, kb0, g.n, sV);
+  ldv.issue(vseq, kb0 + 64, g.n, sV + L::kElems);
+  if (n_iter > 0) issue(0, 0);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kseq, rows_bytes(g.n, a.k_st, D));
+  bf16x8 kf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int64_t key = ka + l32;
+    kf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
+  }
+  if (n_iter > 1) issue(1, 1);
+  constexpr int kLoadsPerIssue = 2 * Loader::kPerWave + 1;
+  auto wait_stage = [&](int it) {
+    if (it + 1 < n_iter)
+      wait_vmcnt<kLoadsPerIssue>();
+    else
+      wait_vmem();
+  };
+
+  f32x16 dkacc[DT], dvacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    dkacc[dt] = f32x16{};
+    dvacc[dt] = f32x16{};
+  }
+  const float c2 = a.scale_log2;
+  const TileLanes<D> tl(lane);
+  // B operand of dP: V rows of this slice
+  const bf16_t* const sVs = sV + (slice >> 1) * L::kElems + tl.op_base + (slice & 1) * 32 * L::kRowElems;
+
+  auto compute = [&](bool masked, int qr, int st) {  // qr = first query row of this wave's half
+    const bf16_t* sQ = stage_q(st);
+    const bf16_t* sdO = stage_o(st);
+    const float* sL = stage_l(st);
+    const float* sD = stage_d(st);
+    f32x16 sc = f32x16{}, dp = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int o = tl.op_base + qh * 32 * L::kRowElems + ks * 16;
+      sc = mfma32(*(const bf16x8*)&sQ[o], kf[ks], sc);
+      dp = mfma32(*(const bf16x8*)&sdO[o], *(const bf16x8*)&sVs[ks * 16], dp);
+    }
+    // rows of sc / dp: query qr + 8*(r/4) + 4*hi + r%4 ; column: the lane's key.
+    if (masked) {
+      // allowed iff qs_lane <= q < nq.  The empty volatile asm keeps this a real
+      // branch, so unmasked tiles do not pay for the compares.
+      __asm__ volatile("");
+      const unsigned base = (unsigned)(qr + 4 * hi - qs_lane);
+      const unsigned lim = (unsigned)(g.nq - qs_lane);
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (base + (unsigned)(8 * (r >> 2) + (r & 3)) >= lim) sc[r] = -INFINITY;
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      f32x8 tp, tds;
+#pragma unroll
+      for (int rg2 = 0; rg2 < 2; ++rg2) {
+        const int rg = 2 * s2 + rg2;
+        const int qr0 = 32 * qh + 8 * rg + 4 * hi;
+        const f32x4 l4 = *(const f32x4*)&sL[qr0];
+        const f32x4 d4 = *(const f32x4*)&sD[qr0];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * rg + e;
+          const float pr = fast_exp2(__builtin_fmaf(sc[r], c2, -l4[e]));
+          tp[4 * rg2 + e] = pr;
+          tds[4 * rg2 + e] = pr * (dp[r] - d4[e]);
+        }
+      }
+      const bf16x8 pb = to_bf16x8(tp);
+      const bf16x8 db = to_bf16x8(tds);
+      const int kk = 2 * qh + s2;  // 16-query step inside the 64-row tile
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int o = tl.tr_base + kk * 16 * L::kRowElems + dt * 32;
+        const bf16x8 ot = cat8(lds_read_tr16(&sdO[o]), lds_read_tr16(&sdO[o + L::kTrSecond]));
+        const bf16x8 qt = cat8(lds_read_tr16(&sQ[o]), lds_read_tr16(&sQ[o + L::kTrSecond]));
+        dvacc[dt] = mfma32(ot, pb, dvacc[dt]);
+        dkacc[dt] = mfma32(qt, db, dkacc[dt]);
+      }
+    }
+  };
+  auto step = [&](int it, int st) {
+    const int hh = it / nqt;
+    const int qr = q_begin + (it - hh * nqt) * kBwdBlockQT + 32 * qh;
+    if (!wave_active || qr + 32 <= w_qs_min || qr >= g.nq) return;
+    compute(qr < w_qs_max || qr + 32 > g.nq, qr, st);
+  };
+
+  // After the barrier of iteration it every wave is done with iteration it - 1,
+  // whose stage ((it + 2) % 3) then receives tile it + 2.
+  for (int it = 0; it < n_iter; it += 3) {
+    wait_stage(it);
+    __syncthreads();
+    if (it + 2 < n_iter) issue(it + 2, 2);
+    step(it, 0);
+    if (it + 1 >= n_iter) break;
+    wait_stage(it + 1);
+    __syncthreads();
+    if (it + 3 < n_iter) issue(it + 3, 0);
+    step(it + 1, 1);
+    if (it + 2 >= n_iter) break;
+    wait_stage(it + 2);
+    __syncthreads();
+    if (it + 4 < n_iter) issue(it + 4, 1);
+    step(it + 2, 2);
+  }
+  // With n_iter == 0 the V / K loads are still in flight here.
+  wait_vmem();
+
+  // Pair reduction: the second wave of each pair hands its partials over
+  // through LDS (lane-major, conflict-free), first dV, then dK.
+  float* part = (float*)smem + slice * 64 * 64 + lane;
+  auto hand_over = [&](f32x16 (&acc)[DT]) {
+    __syncthreads();  // every wave is done with the stage buffers / the previous round
+    if (qh == 1) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[(16 * dt + r) * 64] = acc[dt][r];
+    }
+    __syncthreads();
+    if (qh == 0) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] += part[(16 * dt + r) * 64];
+    }
+  };
+  hand_over(dvacc);
+  hand_over(dkacc);
+
+  if (qh != 0 || !wave_active) return;
+  const int kpos = ka + l32;
+  if (kpos >= g.n) return;
+  bf16_t* krow = a.dk + (int64_t)(g.start + kpos) * a.dk_st + (int64_t)hk * a.dk_sh;
+  bf16_t* vrow = a.dv + (int64_t)(g.start + kpos) * a.dv_st + (int64_t)hk * a.dv_sh;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      f32x4 tk, tv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        tk[e] = dkacc[dt][4 * rg + e] * a.scale;
+        tv[e] = dvacc[dt][4 * rg + e];
+      }
+      *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tk, bf16x4);
+      *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_bwd_dkdv_pair_bf16(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
+  a.num_tiles = (max_seqlen_all + kPairKeys - 1) / kPairKeys;
+  if (numseqs <= 0 || a.num_tiles == 0) return hipSuccess;
+  a.grid_x = a.Hkv * numseqs;
+  hipLaunchKernelGGL(dkdv_pair_kernel, dim3(xcd_spread_width(a.grid_x), a.num_tiles), dim3(kPairWaves * 64), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace mimir
