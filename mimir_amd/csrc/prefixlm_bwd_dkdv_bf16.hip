@@ -104,11 +104,11 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   if (n_iter > 1) issue(1, sQ1, sO1, sL1, sD1);
   // Buffer loads per issue() and wave: Q and dO tiles plus one lse2 / delta row.
   constexpr int kLoadsPerIssue = 2 * TileLoader<D, kDkWaves>::kPerWave + 1;
-  auto wait_stage = [&](int it) {  // tile `it` has landed; tile it + 1 may still be in flight
+  auto sync_stage = [&](int it) {  // tile `it` has landed everywhere; tile it + 1 may still be in flight
     if (it + 1 < n_iter)
-      wait_vmcnt<kLoadsPerIssue>();
+      stage_barrier<kLoadsPerIssue>();
     else
-      wait_vmem();
+      stage_barrier<0>();
   };
 
   f32x16 dkacc[DT], dvacc[DT];
@@ -218,18 +218,15 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   // After the barrier of iteration it every wave is done with iteration it - 1,
   // whose stage ((it + 2) % 3) then receives tile it + 2.
   for (int it = 0; it < n_iter; it += 3) {
-    wait_stage(it);
-    __syncthreads();
+    sync_stage(it);
     if (it + 2 < n_iter) issue(it + 2, sQ2, sO2, sL2, sD2);
     step(it, sQ0, sO0, sL0, sD0);
     if (it + 1 >= n_iter) break;
-    wait_stage(it + 1);
-    __syncthreads();
+    sync_stage(it + 1);
     if (it + 3 < n_iter) issue(it + 3, sQ0, sO0, sL0, sD0);
     step(it + 1, sQ1, sO1, sL1, sD1);
     if (it + 2 >= n_iter) break;
-    wait_stage(it + 2);
-    __syncthreads();
+    sync_stage(it + 2);
     if (it + 4 < n_iter) issue(it + 4, sQ1, sO1, sL1, sD1);
     step(it + 2, sQ2, sO2, sL2, sD2);
   }

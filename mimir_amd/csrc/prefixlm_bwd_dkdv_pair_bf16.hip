@@ -31,21 +31,25 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   using Loader = TileLoader<D, kPairWaves>;
   static_assert(kBwdBlockQT == 64, "one TileLayout tile per Q / dO block");
 
-  // LDS: three stages of (Q tile, dO tile, lse2 row, delta row), then the V tile
-  // (two 64-row TileLayout tiles).  After the tile loop the front of the same
-  // buffer holds the dK / dV partials of the second wave of each pair.
-  constexpr int kTileBytes = L::kElems * 2;
-  constexpr int kStageBytes = 2 * kTileBytes + 2 * kBwdBlockQT * 4;
-  constexpr int kVBytes = 2 * kTileBytes;
-  constexpr int kPartialBytes = 4 * 64 * 64 * 4;  // 4 slices x 64 floats x 64 lanes
-  constexpr int kLdsBytes = 3 * kStageBytes + kVBytes;
-  static_assert(kPartialBytes <= kLdsBytes, "partials reuse the stage buffers");
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kLdsBytes];
-  auto stage_q = [&](int st) { return (bf16_t*)(smem + st * kStageBytes); };
-  auto stage_o = [&](int st) { return (bf16_t*)(smem + st * kStageBytes + kTileBytes); };
-  auto stage_l = [&](int st) { return (float*)(smem + st * kStageBytes + 2 * kTileBytes); };
-  auto stage_d = [&](int st) { return (float*)(smem + st * kStageBytes + 2 * kTileBytes + kBwdBlockQT * 4); };
-  bf16_t* const sV = (bf16_t*)(smem + 3 * kStageBytes);
+  // LDS: three stages of (Q tile, dO tile, lse2 row, delta row) and the V tile
+  // (two 64-row TileLayout tiles), each its own object so that the compiler can
+  // tell the reads of one stage from the tile copies into another.  After the
+  // tile loop the Q / dO tiles of stages 0 and 1 hold the dK / dV partials of
+  // the second wave of each pair.
+  __shared__ __attribute__((aligned(16))) bf16_t sQ0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sO0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sQ1[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sO1[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sQ2[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sO2[L::kElems];
+  __shared__ __attribute__((aligned(16))) float sL0[kBwdBlockQT];
+  __shared__ __attribute__((aligned(16))) float sD0[kBwdBlockQT];
+  __shared__ __attribute__((aligned(16))) float sL1[kBwdBlockQT];
+  __shared__ __attribute__((aligned(16))) float sD1[kBwdBlockQT];
+  __shared__ __attribute__((aligned(16))) float sL2[kBwdBlockQT];
+  __shared__ __attribute__((aligned(16))) float sD2[kBwdBlockQT];
+  __shared__ __attribute__((aligned(16))) bf16_t sV[2 * L::kElems];
+  static_assert(64 * 64 * 4 <= L::kElems * 2, "one slice's partials fit one tile object");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -73,16 +77,16 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   const bf16_t* kseq = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
   const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
   const Loader ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane), ldv(a.v_st, wave, lane);
-  auto issue = [&](int it, int st) {
+  auto issue = [&](int it, bf16_t* tq, bf16_t* to, float* tl, float* td) {
     const int hh = it / nqt;
     const int qb = q_begin + (it - hh * nqt) * kBwdBlockQT;
     const int h = hk * a.group + hh;
-    ldq.issue(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, qb, g.nq, stage_q(st));
-    ldo.issue(a.dout + (int64_t)g.start * a.do_st + (int64_t)h * a.do_sh, qb, g.nq, stage_o(st));
+    ldq.issue(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, qb, g.nq, tq);
+    ldo.issue(a.dout + (int64_t)g.start * a.do_st + (int64_t)h * a.do_sh, qb, g.nq, to);
     // one 4-byte row load per wave: wave 0 lse2, the others delta (same data to the same place)
     const bool lse_row = wave == 0;
     const float* src = lse_row ? a.lse2 : a.delta;
-    float* dst = lse_row ? stage_l(st) : stage_d(st);
+    float* dst = lse_row ? tl : td;
     const __amdgpu_buffer_rsrc_t r = make_rsrc(src + (int64_t)h * a.T + g.start, (uint32_t)g.nq * 4u);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4,
                                              (uint32_t)(qb + lane) * 4u, 0, 0, 0);
@@ -92,7 +96,7 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   // fragments of this wave's slice go to registers.
   ldv.issue(vseq, kb0, g.n, sV);
   ldv.issue(vseq, kb0 + 64, g.n, sV + L::kElems);
-  if (n_iter > 0) issue(0, 0);
+  if (n_iter > 0) issue(0, sQ0, sO0, sL0, sD0);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kseq, rows_bytes(g.n, a.k_st, D));
   bf16x8 kf[KS];
 #pragma unroll
@@ -100,13 +104,13 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
     const int64_t key = ka + l32;
     kf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
   }
-  if (n_iter > 1) issue(1, 1);
+  if (n_iter > 1) issue(1, sQ1, sO1, sL1, sD1);
   constexpr int kLoadsPerIssue = 2 * Loader::kPerWave + 1;
-  auto wait_stage = [&](int it) {
+  auto sync_stage = [&](int it) {  // tile `it` has landed everywhere; tile it + 1 may still be in flight
     if (it + 1 < n_iter)
-      wait_vmcnt<kLoadsPerIssue>();
+      stage_barrier<kLoadsPerIssue>();
     else
-      wait_vmem();
+      stage_barrier<0>();
   };
 
   f32x16 dkacc[DT], dvacc[DT];
@@ -120,11 +124,8 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   // B operand of dP: V rows of this slice
   const bf16_t* const sVs = sV + (slice >> 1) * L::kElems + tl.op_base + (slice & 1) * 32 * L::kRowElems;
 
-  auto compute = [&](bool masked, int qr, int st) {  // qr = first query row of this wave's half
-    const bf16_t* sQ = stage_q(st);
-    const bf16_t* sdO = stage_o(st);
-    const float* sL = stage_l(st);
-    const float* sD = stage_d(st);
+  auto compute = [&](bool masked, int qr, const bf16_t* sQ, const bf16_t* sdO, const float* sL,
+                     const float* sD) {  // qr = first query row of this wave's half
     f32x16 sc = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -173,37 +174,34 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
       }
     }
   };
-  auto step = [&](int it, int st) {
+  auto step = [&](int it, const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
     const int hh = it / nqt;
     const int qr = q_begin + (it - hh * nqt) * kBwdBlockQT + 32 * qh;
     if (!wave_active || qr + 32 <= w_qs_min || qr >= g.nq) return;
-    compute(qr < w_qs_max || qr + 32 > g.nq, qr, st);
+    compute(qr < w_qs_max || qr + 32 > g.nq, qr, sQ, sdO, sL, sD);
   };
 
   // After the barrier of iteration it every wave is done with iteration it - 1,
   // whose stage ((it + 2) % 3) then receives tile it + 2.
   for (int it = 0; it < n_iter; it += 3) {
-    wait_stage(it);
-    __syncthreads();
-    if (it + 2 < n_iter) issue(it + 2, 2);
-    step(it, 0);
+    sync_stage(it);
+    if (it + 2 < n_iter) issue(it + 2, sQ2, sO2, sL2, sD2);
+    step(it, sQ0, sO0, sL0, sD0);
     if (it + 1 >= n_iter) break;
-    wait_stage(it + 1);
-    __syncthreads();
-    if (it + 3 < n_iter) issue(it + 3, 0);
-    step(it + 1, 1);
+    sync_stage(it + 1);
+    if (it + 3 < n_iter) issue(it + 3, sQ0, sO0, sL0, sD0);
+    step(it + 1, sQ1, sO1, sL1, sD1);
     if (it + 2 >= n_iter) break;
-    wait_stage(it + 2);
-    __syncthreads();
-    if (it + 4 < n_iter) issue(it + 4, 1);
-    step(it + 2, 2);
+    sync_stage(it + 2);
+    if (it + 4 < n_iter) issue(it + 4, sQ1, sO1, sL1, sD1);
+    step(it + 2, sQ2, sO2, sL2, sD2);
   }
   // With n_iter == 0 the V / K loads are still in flight here.
   wait_vmem();
 
   // Pair reduction: the second wave of each pair hands its partials over
   // through LDS (lane-major, conflict-free), first dV, then dK.
-  float* part = (float*)smem + slice * 64 * 64 + lane;
+  float* const part = (float*)(slice == 0 ? sQ0 : slice == 1 ? sO0 : slice == 2 ? sQ1 : sO1) + lane;
   auto hand_over = [&](f32x16 (&acc)[DT]) {
     __syncthreads();  // every wave is done with the stage buffers / the previous round
     if (qh == 1) {

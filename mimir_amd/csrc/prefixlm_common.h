@@ -242,6 +242,22 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
+// Barrier of a multi-stage LDS pipeline: this wave's LDS reads are complete and
+// at most N of its vector-memory operations (the newest tile copies) are still
+// in flight, then all waves meet.  Unlike __syncthreads(), whose workgroup
+// release fence makes the compiler wait for every outstanding buffer -> LDS
+// copy (vmcnt(0)), the tiles issued for later stages stay in flight across it.
+// The empty asm statements keep the compiler from moving memory accesses
+// across the barrier.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate (low field)");
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0070 | N);  // vmcnt(N) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
 }  // namespace mimir
 
 // Internal launchers (implemented per kernel file, dispatched from prefixlm_capi.cpp).
