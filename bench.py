@@ -250,7 +250,8 @@ def main() -> int:
     value = flops / (ms_per_step * 1e-3) / 1e12
     peak = PEAK_F32_TFLOPS if c.q.dtype == torch.float32 else PEAK_BF16_TFLOPS
     kernel_flops = {"fwd": f_fwd, "dkdv": 8.0 * d * hq * pairs, "dq": 2.0 * d * hq * pairs}
-    kernel_names = {"fwd": "fwd_bf16_kernel" if elem == 2 else "fwd_f32_kernel", "dkdv": "dkdv_kernel",
+    kernel_names = {"fwd": "fwd_bf16_kernel" if elem == 2 else "fwd_f32_kernel",
+                    "dkdv": "dkdv_pair_kernel" if (elem == 2 and d == 128) else "dkdv_kernel",
                     "dq": "dq_kernel"}
     dom = max((n for n in kernel_flops if n in stage_avg), key=lambda n: stage_avg[n])
     achieved = kernel_flops[dom] / (stage_avg[dom] * 1e-3) / 1e12
