@@ -151,3 +151,33 @@ def test_empty_batch_is_all_padding(device, dtype):
     assert torch.count_nonzero(got["o"]) == 0 and torch.isneginf(got["lse"]).all()
     for key in ("dq", "dk", "dv"):
         assert torch.count_nonzero(got[key]) == 0, key
+
+
+def test_backward_matches_its_stages(device):
+    """mimir_prefixlm_bwd must equal, bitwise, its stages called one at a time."""
+    import ctypes
+
+    from mimir_amd import _capi
+    from mimir_amd import prefixlm as P
+
+    case = make_case([700, 300, 45], [350, 0, 45], 8, 2, 128, seed=11, dtype=torch.bfloat16)
+    c = case.to(device)
+    lib = _capi.load()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    scale = 1.0 / 128 ** 0.5
+    fp, out, lse, _kf = P.prepare_fwd(c.q, c.k, c.v, False, c.prefix_lens, c.causal_lens, c.cu_seqlens,
+                                      c.total_seqlen, c.numseqs, c.max_seqlen_all, scale)
+    _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(fp), stream))
+    grads = []
+    for serial in (False, True):
+        bp, dq, dk, dv, _kb = P.prepare_bwd(c.dout, c.q, c.k, c.v, out, lse, False, c.prefix_lens, c.causal_lens,
+                                            c.cu_seqlens, c.total_seqlen, c.numseqs, c.max_seqlen_all, scale)
+        if serial:
+            for bits in (_capi.BWD_STAGE_DELTA, _capi.BWD_STAGE_DKDV, _capi.BWD_STAGE_DQ, _capi.BWD_STAGE_FILL):
+                _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd_stages(ctypes.byref(bp), bits, stream))
+        else:
+            _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd(ctypes.byref(bp), stream))
+        torch.cuda.synchronize()
+        grads.append((dq.clone(), dk.clone(), dv.clone()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
