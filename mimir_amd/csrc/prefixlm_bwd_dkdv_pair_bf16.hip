@@ -77,26 +77,47 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   const bf16_t* kseq = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
   const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
   const Loader ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane), ldv(a.v_st, wave, lane);
-  auto issue = [&](int it, bf16_t* tq, bf16_t* to, float* tl, float* td) {
-    const int hh = it / nqt;
-    const int qb = q_begin + (it - hh * nqt) * kBwdBlockQT;
-    const int h = hk * a.group + hh;
-    ldq.issue(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, qb, g.nq, tq);
-    ldo.issue(a.dout + (int64_t)g.start * a.do_st + (int64_t)h * a.do_sh, qb, g.nq, to);
-    // one 4-byte row load per wave: wave 0 lse2, the others delta (same data to the same place)
-    const bool lse_row = wave == 0;
-    const float* src = lse_row ? a.lse2 : a.delta;
-    float* dst = lse_row ? tl : td;
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(src + (int64_t)h * a.T + g.start, (uint32_t)g.nq * 4u);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4,
-                                             (uint32_t)(qb + lane) * 4u, 0, 0, 0);
+
+  // Iteration it covers q head hk * G + it / nqt and query tile it % nqt.  The
+  // tile copies walk that order with running addresses (adds only), which keeps
+  // the scalar work between barrier and first MFMA short.
+  const uint32_t q_st32 = (uint32_t)a.q_st, o_st32 = (uint32_t)a.do_st;
+  const bf16_t* q_head = a.q + ((int64_t)g.start + q_begin) * a.q_st + (int64_t)(hk * a.group) * a.q_sh;
+  const bf16_t* o_head = a.dout + ((int64_t)g.start + q_begin) * a.do_st + (int64_t)(hk * a.group) * a.do_sh;
+  // one 4-byte row per wave: wave 0 lse2, the others delta (same data to the same place)
+  const float* r_head = (wave == 0 ? a.lse2 : a.delta) + (int64_t)(hk * a.group) * a.T + g.start + q_begin;
+  const bf16_t* i_q = q_head;
+  const bf16_t* i_o = o_head;
+  const float* i_r = r_head;
+  int i_qt = 0, i_rows = g.nq - q_begin;
+  auto issue_next = [&](bf16_t* tq, bf16_t* to, float* tl, float* td) {
+    ldq.issue_at(i_q, rows_bytes32(i_rows, q_st32, D), tq);
+    ldo.issue_at(i_o, rows_bytes32(i_rows, o_st32, D), to);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(i_r, i_rows > 0 ? (uint32_t)i_rows * 4u : 0u);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(wave == 0 ? tl : td), 4,
+                                             (uint32_t)lane * 4u, 0, 0, 0);
+    if (++i_qt == nqt) {
+      i_qt = 0;
+      i_rows = g.nq - q_begin;
+      q_head += a.q_sh;
+      o_head += a.do_sh;
+      r_head += a.T;
+      i_q = q_head;
+      i_o = o_head;
+      i_r = r_head;
+    } else {
+      i_rows -= kBwdBlockQT;
+      i_q += kBwdBlockQT * a.q_st;
+      i_o += kBwdBlockQT * a.do_st;
+      i_r += kBwdBlockQT;
+    }
   };
 
   // V tile (keys kb0 .. kb0 + 127), then the first two Q / dO stages; the K
   // fragments of this wave's slice go to registers.
   ldv.issue(vseq, kb0, g.n, sV);
   ldv.issue(vseq, kb0 + 64, g.n, sV + L::kElems);
-  if (n_iter > 0) issue(0, sQ0, sO0, sL0, sD0);
+  if (n_iter > 0) issue_next(sQ0, sO0, sL0, sD0);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kseq, rows_bytes(g.n, a.k_st, D));
   bf16x8 kf[KS];
 #pragma unroll
@@ -104,7 +125,7 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
     const int64_t key = ka + l32;
     kf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
   }
-  if (n_iter > 1) issue(1, sQ1, sO1, sL1, sD1);
+  if (n_iter > 1) issue_next(sQ1, sO1, sL1, sD1);
   constexpr int kLoadsPerIssue = 2 * Loader::kPerWave + 1;
   auto sync_stage = [&](int it) {  // tile `it` has landed everywhere; tile it + 1 may still be in flight
     if (it + 1 < n_iter)
@@ -174,9 +195,10 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
       }
     }
   };
-  auto step = [&](int it, const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
-    const int hh = it / nqt;
-    const int qr = q_begin + (it - hh * nqt) * kBwdBlockQT + 32 * qh;
+  int s_qt = 0;  // query tile of the next step (the head only matters to the copies)
+  auto step = [&](const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
+    const int qr = q_begin + s_qt * kBwdBlockQT + 32 * qh;
+    if (++s_qt == nqt) s_qt = 0;
     if (!wave_active || qr + 32 <= w_qs_min || qr >= g.nq) return;
     compute(qr < w_qs_max || qr + 32 > g.nq, qr, sQ, sdO, sL, sD);
   };
@@ -185,16 +207,16 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   // whose stage ((it + 2) % 3) then receives tile it + 2.
   for (int it = 0; it < n_iter; it += 3) {
     sync_stage(it);
-    if (it + 2 < n_iter) issue(it + 2, sQ2, sO2, sL2, sD2);
-    step(it, sQ0, sO0, sL0, sD0);
+    if (it + 2 < n_iter) issue_next(sQ2, sO2, sL2, sD2);
+    step(sQ0, sO0, sL0, sD0);
     if (it + 1 >= n_iter) break;
     sync_stage(it + 1);
-    if (it + 3 < n_iter) issue(it + 3, sQ0, sO0, sL0, sD0);
-    step(it + 1, sQ1, sO1, sL1, sD1);
+    if (it + 3 < n_iter) issue_next(sQ0, sO0, sL0, sD0);
+    step(sQ1, sO1, sL1, sD1);
     if (it + 2 >= n_iter) break;
     sync_stage(it + 2);
-    if (it + 4 < n_iter) issue(it + 4, sQ1, sO1, sL1, sD1);
-    step(it + 2, sQ2, sO2, sL2, sD2);
+    if (it + 4 < n_iter) issue_next(sQ1, sO1, sL1, sD1);
+    step(sQ2, sO2, sL2, sD2);
   }
   // With n_iter == 0 the V / K loads are still in flight here.
   wait_vmem();

@@ -88,6 +88,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 __device__ __forceinline__ uint32_t rows_bytes(int rows, int64_t stride, int d) {
   return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + d) * 2) : 0u;
 }
+// 32-bit form for tiles inside one tensor (the C ABI bounds every span by 2 GiB).
+__device__ __forceinline__ uint32_t rows_bytes32(int rows, uint32_t stride, int d) {
+  return rows > 0 ? ((uint32_t)(rows - 1) * stride + (uint32_t)d) * 2u : 0u;
+}
 
 __device__ __forceinline__ i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
@@ -205,7 +209,11 @@ struct TileLoader {
   }
   // Copy rows [row0, row0 + 64) of the matrix at `base`; rows >= nrows read as 0.
   __device__ __forceinline__ void issue(const bf16_t* base, int row0, int nrows, bf16_t* tile) const {
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(base + (int64_t)row0 * st, rows_bytes(nrows - row0, st, D));
+    issue_at(base + (int64_t)row0 * st, rows_bytes(nrows - row0, st, D), tile);
+  }
+  // Same, from the first row's address and the byte size of the rows left.
+  __device__ __forceinline__ void issue_at(const bf16_t* first_row, uint32_t bytes, bf16_t* tile) const {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(first_row, bytes);
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(tile + lds[i]), 16,
