@@ -58,11 +58,18 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
   const TileLoader<D, kWaves> ldk(a.k_st, wave, lane), ldv(a.v_st, wave, lane);
 
-  auto issue = [&](int kt, bf16_t* tk, bf16_t* tv) {
-    ldk.issue(kseq, kt * kBlockK, g.n, tk);
-    ldv.issue(vseq, kt * kBlockK, g.n, tv);
+  // Tile copies walk the key tiles in order with running addresses (adds only).
+  const bf16_t* i_k = kseq;
+  const bf16_t* i_v = vseq;
+  int i_rows = g.n;
+  auto issue_next = [&](bf16_t* tk, bf16_t* tv) {
+    ldk.issue_at(i_k, rows_bytes32(i_rows, (uint32_t)a.k_st, D), tk);
+    ldv.issue_at(i_v, rows_bytes32(i_rows, (uint32_t)a.v_st, D), tv);
+    i_k += kBlockK * a.k_st;
+    i_v += kBlockK * a.v_st;
+    i_rows -= kBlockK;
   };
-  issue(0, sK0, sV0);
+  issue_next(sK0, sV0);
 
   bf16x8 qf[KS], dof[KS];
 #pragma unroll
@@ -143,12 +150,12 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   for (int kt = 0; kt < nkt; kt += 2) {
     wait_vmem();
     __syncthreads();
-    if (kt + 1 < nkt) issue(kt + 1, sK1, sV1);
+    if (kt + 1 < nkt) issue_next(sK1, sV1);
     compute(kt, sK0, sV0);
     if (kt + 1 >= nkt) break;
     wait_vmem();
     __syncthreads();
-    if (kt + 2 < nkt) issue(kt + 2, sK0, sV0);
+    if (kt + 2 < nkt) issue_next(sK0, sV0);
     compute(kt + 1, sK1, sV1);
   }
 

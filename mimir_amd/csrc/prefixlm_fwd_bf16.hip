@@ -96,11 +96,18 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
   const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
   const TileLoader<D, kWaves> ldk(a.k_st, wave, lane), ldv(a.v_st, wave, lane);
 
-  auto issue = [&](int kt, bf16_t* tk, bf16_t* tv) {
-    ldk.issue(kseq, kt * kBlockN, g.n, tk);
-    ldv.issue(vseq, kt * kBlockN, g.n, tv);
+  // Tile copies walk the key tiles in order with running addresses (adds only).
+  const bf16_t* i_k = kseq;
+  const bf16_t* i_v = vseq;
+  int i_rows = g.n;
+  auto issue_next = [&](bf16_t* tk, bf16_t* tv) {
+    ldk.issue_at(i_k, rows_bytes32(i_rows, (uint32_t)a.k_st, D), tk);
+    ldv.issue_at(i_v, rows_bytes32(i_rows, (uint32_t)a.v_st, D), tv);
+    i_k += kBlockN * a.k_st;
+    i_v += kBlockN * a.v_st;
+    i_rows -= kBlockN;
   };
-  issue(0, sK0, sV0);
+  issue_next(sK0, sV0);
 
   // Q^T B-operand fragments: lane holds query qpos, d = 16*ks + 8*hi .. +7.
   bf16x8 qf[KS];
@@ -212,12 +219,12 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
   for (int kt = 0; kt < nkt; kt += 2) {
     wait_vmem();
     __syncthreads();
-    if (kt + 1 < nkt) issue(kt + 1, sK1, sV1);
+    if (kt + 1 < nkt) issue_next(sK1, sV1);
     step(kt, sK0, sV0);
     if (kt + 1 >= nkt) break;
     wait_vmem();
     __syncthreads();
-    if (kt + 2 < nkt) issue(kt + 2, sK0, sV0);
+    if (kt + 2 < nkt) issue_next(sK0, sV0);
     step(kt + 1, sK1, sV1);
   }
 
