@@ -148,12 +148,16 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   auto compute = [&](bool masked, int qr, const bf16_t* sQ, const bf16_t* sdO, const float* sL,
                      const float* sD) {  // qr = first query row of this wave's half
     f32x16 sc = f32x16{}, dp = f32x16{};
+    // S / dP MFMAs at raised wave priority: of the two waves on a SIMD, the one
+    // ready to issue MFMAs goes first while the other runs its softmax.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int o = tl.op_base + qh * 32 * L::kRowElems + ks * 16;
       sc = mfma32(*(const bf16x8*)&sQ[o], kf[ks], sc);
       dp = mfma32(*(const bf16x8*)&sdO[o], *(const bf16x8*)&sVs[ks * 16], dp);
     }
+    __builtin_amdgcn_s_setprio(0);
     // rows of sc / dp: query qr + 8*(r/4) + 4*hi + r%4 ; column: the lane's key.
     if (masked) {
       // allowed iff qs_lane <= q < nq.  The empty volatile asm keeps this a real
