@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MIMIR_PREFIXLM_ABI_VERSION 1
+#define MIMIR_PREFIXLM_ABI_VERSION 2
 
 /* Element types of q/k/v/out/dout/dq/dk/dv (lse and the workspace are float32). */
 enum MimirDType {
@@ -84,6 +84,8 @@ typedef struct MimirPrefixLMFwdParams {
   int32_t is_causal;
   int32_t dtype;              /* enum MimirDType */
   float softmax_scale;        /* > 0; the reference uses 1/sqrt(D) */
+  void* workspace;            /* device memory, >= mimir_prefixlm_fwd_workspace_bytes(); 16-byte aligned */
+  size_t workspace_bytes;
 } MimirPrefixLMFwdParams;
 
 typedef struct MimirPrefixLMBwdParams {
@@ -122,6 +124,10 @@ typedef struct MimirPrefixLMBwdParams {
   size_t workspace_bytes;
 } MimirPrefixLMBwdParams;
 
+/* Bytes of device workspace the forward needs: the heaviest-first tile work list
+ * (int32 pairs, one per 128-row query tile of every sequence). */
+size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs, int32_t max_seqlen_all);
+
 /* Forward: out (and lse if non-NULL).
  * Replaces the FA4 two-pass forward, src/mimir/model/flash_attention_prefixlm_fa4.py:353-406
  * (+ _fa4_varlen, fa4.py:17-50), the FA3 forward custom op
@@ -150,8 +156,10 @@ enum MimirBwdStage {
 int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* params, int stages, void* stream);
 
 /* Bytes of device workspace the backward needs: float32 delta = rowsum(O * dO) [Hq, T]
- * and float32 lse * log2(e) [Hq, T], both written by the DELTA stage. */
-size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads);
+ * and float32 lse * log2(e) [Hq, T], both written by the DELTA stage, then the
+ * tile work lists of the DQ and DKDV stages (each written by its stage). */
+size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads, int32_t numseqs,
+                                          int32_t max_seqlen_all);
 
 /* Device-side metadata check: writes to *bad_seq (device int32) the first s in
  * [0, numseqs) with prefix_lens[s] + causal_lens[s] != cu_seqlens[s+1] - cu_seqlens[s]

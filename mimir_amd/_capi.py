@@ -16,7 +16,7 @@ from pathlib import Path
 
 # MIMIR_PREFIXLM_LIB overrides the in-tree library (e.g. to A/B two builds).
 LIB_PATH = Path(os.environ.get("MIMIR_PREFIXLM_LIB") or Path(__file__).resolve().parent / "_lib" / "libmimir_prefixlm.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_FLOAT32 = 0
 DTYPE_BFLOAT16 = 1
@@ -44,6 +44,7 @@ class FwdParams(ctypes.Structure):
         ("total_tokens", _i32), ("num_q_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
         ("numseqs", _i32), ("total_seqlen", _i32), ("max_seqlen_all", _i32), ("is_causal", _i32),
         ("dtype", _i32), ("softmax_scale", ctypes.c_float),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -78,6 +79,7 @@ EXPORTED_SYMBOLS = (
     "mimir_prefixlm_fwd",
     "mimir_prefixlm_bwd",
     "mimir_prefixlm_bwd_stages",
+    "mimir_prefixlm_fwd_workspace_bytes",
     "mimir_prefixlm_bwd_workspace_bytes",
     "mimir_prefixlm_check_metadata",
     "mimir_prefixlm_last_error",
@@ -112,7 +114,9 @@ def load() -> ctypes.CDLL:
         lib.mimir_prefixlm_bwd.restype = ctypes.c_int
         lib.mimir_prefixlm_bwd_stages.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int, _vp]
         lib.mimir_prefixlm_bwd_stages.restype = ctypes.c_int
-        lib.mimir_prefixlm_bwd_workspace_bytes.argtypes = [_i32, _i32]
+        lib.mimir_prefixlm_fwd_workspace_bytes.argtypes = [_i32, _i32, _i32]
+        lib.mimir_prefixlm_fwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.mimir_prefixlm_bwd_workspace_bytes.argtypes = [_i32, _i32, _i32, _i32]
         lib.mimir_prefixlm_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mimir_prefixlm_check_metadata.argtypes = [_vp, _vp, _vp, _i32, _vp, _vp]
         lib.mimir_prefixlm_check_metadata.restype = ctypes.c_int

@@ -31,8 +31,10 @@ struct BwdArgs {
   int group;
   int total_seqlen;
   int is_causal;
-  int num_tiles;     // grid y extent of the launched kernel
-  int grid_x;        // valid blockIdx.x values of the launched kernel
+  int2* plan_q;      // workspace: query-tile work list (dQ stage)
+  int2* plan_k;      // workspace: key-tile work list (dK / dV stage)
+  int plan_cap;      // entries of each list (plan_capacity)
+  const int2* plan;  // the list the launched kernel reads
   float scale;
   float scale_log2;
 };

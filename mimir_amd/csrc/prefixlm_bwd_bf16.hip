@@ -70,6 +70,10 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stage
   a.dv = (bf16_t*)p.dv;
   a.delta = (float*)p.workspace;
   a.lse2 = (float*)p.workspace + (int64_t)p.num_q_heads * p.total_tokens;
+  a.plan_cap = plan_capacity(p.total_tokens, p.numseqs, p.max_seqlen_all);
+  a.plan_q = (int2*)((float*)p.workspace + 2 * (int64_t)p.num_q_heads * p.total_tokens);
+  a.plan_k = a.plan_q + a.plan_cap;
+  a.plan = nullptr;
   a.prefix_lens = p.prefix_lens;
   a.cu_seqlens = p.cu_seqlens;
   a.q_st = p.q_stride_token; a.q_sh = p.q_stride_head;
@@ -87,7 +91,6 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stage
   a.group = p.num_q_heads / p.num_kv_heads;
   a.total_seqlen = p.total_seqlen;
   a.is_causal = p.is_causal;
-  a.num_tiles = 0;
   a.scale = p.softmax_scale;
   a.scale_log2 = p.softmax_scale * kLog2e;
 

@@ -11,7 +11,8 @@ namespace {
 // dV^T += dO^T P and dK^T += Q^T dS directly, and the transposed dO^T / Q^T
 // fragments come from the row-major LDS tiles via ds_read_b64_tr_b16.
 // The query range starts at qstart(first key) = (key < p ? 0 : key).
-// Grid: x = sequence * Hkv + kv head, y = key tile (prefix keys, the heaviest, first).
+// Workgroup r * Hkv + h takes kv head h of entry r of the key-tile work list
+// (prefixlm_plan.hip): the heaviest key tiles first.
 //
 // At head_dim 128 the K / V fragments and the dK / dV accumulators allow one
 // wave per SIMD, so LDS latency is hidden inside the wave: every operand
@@ -50,10 +51,12 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-  if ((int)blockIdx.x >= a.grid_x) return;
-  const int hk = blockIdx.x % a.Hkv;
-  const int s = blockIdx.x / a.Hkv;
-  const int ktile = blockIdx.y;
+  const int rank = blockIdx.x / a.Hkv;
+  const int hk = blockIdx.x - rank * a.Hkv;
+  const int2 item = a.plan[rank];
+  if (item.x < 0) return;  // list padding
+  const int s = item.x;
+  const int ktile = item.y;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int kb0 = ktile * kDkKeys;
   if (kb0 >= g.n) return;
@@ -255,10 +258,14 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
 template <int D>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   constexpr int kDkKeys = DkCfg<D>::kKeys, kDkWaves = DkCfg<D>::kWaves;
-  a.num_tiles = (max_seqlen_all + kDkKeys - 1) / kDkKeys;
-  if (numseqs <= 0 || a.num_tiles == 0) return hipSuccess;
-  a.grid_x = a.Hkv * numseqs;
-  hipLaunchKernelGGL(dkdv_kernel<D>, dim3(xcd_spread_width(a.grid_x), a.num_tiles), dim3(kDkWaves * 64), 0,
+  static_assert(kDkKeys == kPlanTile, "work-list tiles are the dK / dV key tiles");
+  if (numseqs <= 0 || a.plan_cap == 0) return hipSuccess;
+  hipError_t e = launch_plan(a.cu_seqlens, a.prefix_lens, numseqs, a.total_seqlen, a.is_causal, a.T, /*kind=*/1,
+                             a.group, a.plan_cap, a.plan_k, stream);
+  if (e != hipSuccess) return e;
+  a.plan = a.plan_k;
+  // workgroup r * Hkv + h: list entry r, kv head h
+  hipLaunchKernelGGL((dkdv_kernel<D>), dim3((unsigned)a.plan_cap * (unsigned)a.Hkv), dim3(kDkWaves * 64), 0,
                      stream, a);
   return hipGetLastError();
 }

@@ -58,11 +58,13 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   const int qh = wave >> 2;    // 32-query half of each tile
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-  if ((int)blockIdx.x >= a.grid_x) return;
-  const int hk = blockIdx.x % a.Hkv;
-  const int s = blockIdx.x / a.Hkv;
+  const int rank = blockIdx.x / a.Hkv;
+  const int hk = blockIdx.x - rank * a.Hkv;
+  const int2 item = a.plan[rank];
+  if (item.x < 0) return;  // list padding
+  const int s = item.x;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
-  const int kb0 = blockIdx.y * kPairKeys;
+  const int kb0 = item.y * kPairKeys;
   if (kb0 >= g.n) return;
 
   const int ka = kb0 + slice * 32;  // first key of this wave's slice
@@ -270,10 +272,14 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
 }  // namespace
 
 hipError_t launch_bwd_dkdv_pair_bf16(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
-  a.num_tiles = (max_seqlen_all + kPairKeys - 1) / kPairKeys;
-  if (numseqs <= 0 || a.num_tiles == 0) return hipSuccess;
-  a.grid_x = a.Hkv * numseqs;
-  hipLaunchKernelGGL(dkdv_pair_kernel, dim3(xcd_spread_width(a.grid_x), a.num_tiles), dim3(kPairWaves * 64), 0,
+  static_assert(kPairKeys == kPlanTile, "work-list tiles are the dK / dV key tiles");
+  if (numseqs <= 0 || a.plan_cap == 0) return hipSuccess;
+  hipError_t e = launch_plan(a.cu_seqlens, a.prefix_lens, numseqs, a.total_seqlen, a.is_causal, a.T, /*kind=*/1,
+                             a.group, a.plan_cap, a.plan_k, stream);
+  if (e != hipSuccess) return e;
+  a.plan = a.plan_k;
+  // workgroup r * Hkv + h: list entry r, kv head h
+  hipLaunchKernelGGL(dkdv_pair_kernel, dim3((unsigned)a.plan_cap * (unsigned)a.Hkv), dim3(kPairWaves * 64), 0,
                      stream, a);
   return hipGetLastError();
 }

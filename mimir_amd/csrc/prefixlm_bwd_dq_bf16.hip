@@ -14,7 +14,8 @@ constexpr int kBlockK = 64;   // keys per LDS tile
 // dQ.  Mirrors the forward's S^T formulation: each lane owns one query column,
 // so lse and delta are lane-local and dS^T feeds the B operand of dQ^T += K^T dS^T
 // directly; K^T fragments come from the row-major K tile via ds_read_b64_tr_b16.
-// Grid: x = sequence * Hq + head, y = query tile (reversed: longest key ranges first).
+// Workgroup r * Hq + h takes head h of entry r of the query-tile work list
+// (prefixlm_plan.hip): longest key ranges first.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
@@ -32,10 +33,12 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-  if ((int)blockIdx.x >= a.grid_x) return;
-  const int h = blockIdx.x % a.Hq;
-  const int s = blockIdx.x / a.Hq;
-  const int qtile = a.num_tiles - 1 - (int)blockIdx.y;
+  const int rank = blockIdx.x / a.Hq;
+  const int h = blockIdx.x - rank * a.Hq;
+  const int2 item = a.plan[rank];
+  if (item.x < 0) return;  // list padding
+  const int s = item.x;
+  const int qtile = item.y;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = qtile * kBlockQ;
   if (m0 >= g.nq) return;
@@ -175,10 +178,14 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
 
 template <int D>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
-  a.num_tiles = (max_seqlen_all + kBlockQ - 1) / kBlockQ;
-  if (numseqs <= 0 || a.num_tiles == 0) return hipSuccess;
-  a.grid_x = a.Hq * numseqs;
-  hipLaunchKernelGGL(dq_kernel<D>, dim3(xcd_spread_width(a.grid_x), a.num_tiles), dim3(kThreads), 0, stream, a);
+  static_assert(kBlockQ == kPlanTile, "work-list tiles are the dQ query tiles");
+  if (numseqs <= 0 || a.plan_cap == 0) return hipSuccess;
+  hipError_t e = launch_plan(a.cu_seqlens, a.prefix_lens, numseqs, a.total_seqlen, a.is_causal, a.T, /*kind=*/0,
+                             a.group, a.plan_cap, a.plan_q, stream);
+  if (e != hipSuccess) return e;
+  a.plan = a.plan_q;
+  // workgroup r * Hq + h: list entry r, head h
+  hipLaunchKernelGGL(dq_kernel<D>, dim3((unsigned)a.plan_cap * (unsigned)a.Hq), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

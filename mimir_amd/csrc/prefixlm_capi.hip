@@ -144,10 +144,17 @@ const char* mimir_prefixlm_last_error(void) { return g_last_error.c_str(); }
 
 int mimir_prefixlm_abi_version(void) { return MIMIR_PREFIXLM_ABI_VERSION; }
 
-size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads) {
+size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs, int32_t max_seqlen_all) {
+  if (total_tokens <= 0) return 0;
+  return (size_t)mimir::plan_capacity(total_tokens, numseqs, max_seqlen_all) * sizeof(int2);
+}
+
+size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads, int32_t numseqs,
+                                          int32_t max_seqlen_all) {
   if (total_tokens <= 0 || num_q_heads <= 0) return 0;
-  // float32 delta [Hq, T] followed by float32 lse * log2(e) [Hq, T]
-  return 2 * (size_t)total_tokens * (size_t)num_q_heads * sizeof(float);
+  // float32 delta [Hq, T], float32 lse * log2(e) [Hq, T], then the dQ and dK/dV tile lists
+  return 2 * (size_t)total_tokens * (size_t)num_q_heads * sizeof(float) +
+         2 * (size_t)mimir::plan_capacity(total_tokens, numseqs, max_seqlen_all) * sizeof(int2);
 }
 
 int mimir_prefixlm_check_metadata(const int32_t* prefix_lens, const int32_t* causal_lens,
@@ -180,6 +187,10 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* p, void* stream_) {
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "metadata pointer is NULL");
   if (p->lse != nullptr && p->lse_stride_head < p->total_tokens)
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "lse head stride is smaller than the packed length");
+  const size_t need = mimir_prefixlm_fwd_workspace_bytes(p->total_tokens, p->numseqs, p->max_seqlen_all);
+  if (need > 0 && (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace)))
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +
+                                                std::to_string(need) + " bytes");
   hipError_t e = dt == MIMIR_DTYPE_BFLOAT16 ? mimir_launch_fwd_bf16(*p, stream) : mimir_launch_fwd_f32(*p, stream);
   if ((rc = hip_status(e, "forward launch"))) return rc;
   e = launch_fill(p->out, p->out_stride_token, p->out_stride_head, p->lse, p->lse_stride_head, p->cu_seqlens,
@@ -214,7 +225,8 @@ int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* p, int stages, void*
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "lse head stride is smaller than the packed length");
   if (p->numseqs > 0 && (p->prefix_lens == nullptr || p->cu_seqlens == nullptr))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "metadata pointer is NULL");
-  const size_t need = mimir_prefixlm_bwd_workspace_bytes(p->total_tokens, p->num_q_heads);
+  const size_t need =
+      mimir_prefixlm_bwd_workspace_bytes(p->total_tokens, p->num_q_heads, p->numseqs, p->max_seqlen_all);
   if (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +
                                                 std::to_string(need) + " bytes");

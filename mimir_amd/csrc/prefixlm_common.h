@@ -268,6 +268,18 @@ __device__ __forceinline__ void stage_barrier() {
 
 }  // namespace mimir
 
+namespace mimir {
+// Tile work lists (prefixlm_plan.hip).  kind 0: 128-row query tiles (forward,
+// dQ); kind 1: 128-key tiles (dK / dV).  The list of capacity plan_capacity()
+// int2 (sequence, tile) entries is sorted by cost, descending, and padded with
+// (-1, -1); workgroup r * H + h of a consumer takes entry r for head h.
+constexpr int kPlanTile = 128;
+int plan_capacity(int total_tokens, int numseqs, int max_seqlen_all);
+hipError_t launch_plan(const int32_t* cu_seqlens, const int32_t* prefix_lens, int numseqs, int total_seqlen,
+                       int is_causal, int total_tokens, int kind, int group, int cap, int2* items,
+                       hipStream_t stream);
+}  // namespace mimir
+
 // Internal launchers (implemented per kernel file, dispatched from prefixlm_capi.cpp).
 hipError_t mimir_launch_fwd_bf16(const MimirPrefixLMFwdParams& p, hipStream_t stream);
 hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages);

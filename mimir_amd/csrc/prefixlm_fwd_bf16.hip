@@ -1,8 +1,8 @@
 // bf16 prefix-LM attention forward for gfx950 (MI355X).
 //
 // One workgroup = 4 waves = 128 query rows of one (sequence, query head); each
-// wave owns 32 rows.  Grid: x = sequence * Hq + head, y = query tile counted from
-// the end of the sequence, so the tiles with the longest key ranges go first.
+// wave owns 32 rows.  Workgroup r * Hq + h takes head h of entry r of the tile
+// work list (prefixlm_plan.hip): query tiles sorted by key range, longest first.
 //
 // The kernel computes S^T = K Q^T on v_mfma_f32_32x32x16_bf16 so that every lane
 // holds one query column of the score tile: the softmax max/sum over keys is a
@@ -44,8 +44,7 @@ struct FwdArgs {
   int group;         // Hq / Hkv
   int total_seqlen;
   int is_causal;
-  int num_m_tiles;
-  int grid_x;        // valid blockIdx.x values: Hq * numseqs
+  const int2* plan;  // (sequence, query tile) per workgroup row, heaviest first (prefixlm_plan.hip)
   float scale;       // softmax scale
   float scale_log2;  // softmax scale * log2(e)
 };
@@ -70,10 +69,12 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
-  if ((int)blockIdx.x >= a.grid_x) return;
-  const int h = blockIdx.x % a.Hq;
-  const int s = blockIdx.x / a.Hq;
-  const int mtile = a.num_m_tiles - 1 - (int)blockIdx.y;  // longest key ranges first
+  const int rank = blockIdx.x / a.Hq;
+  const int h = blockIdx.x - rank * a.Hq;
+  const int2 item = a.plan[rank];
+  if (item.x < 0) return;  // list padding
+  const int s = item.x;
+  const int mtile = item.y;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = mtile * kBlockM;
   if (m0 >= g.nq) return;
@@ -267,14 +268,19 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
   a.group = p.num_q_heads / p.num_kv_heads;
   a.total_seqlen = p.total_seqlen;
   a.is_causal = p.is_causal;
-  a.num_m_tiles = (p.max_seqlen_all + kBlockM - 1) / kBlockM;
   a.scale = p.softmax_scale;
   a.scale_log2 = p.softmax_scale * kLog2e;
-  if (a.num_m_tiles == 0 || p.numseqs == 0) return hipSuccess;
-  // x = sequence * Hq + head (GQA siblings adjacent), y = query tile, heaviest first
-  a.grid_x = p.num_q_heads * p.numseqs;
-  dim3 grid(xcd_spread_width(a.grid_x), a.num_m_tiles);
-  hipLaunchKernelGGL(fwd_bf16_kernel<D>, grid, dim3(kThreads), 0, stream, a);
+  static_assert(kBlockM == kPlanTile, "work-list tiles are the forward's query tiles");
+  const int cap = plan_capacity(p.total_tokens, p.numseqs, p.max_seqlen_all);
+  if (cap == 0) return hipSuccess;
+  int2* plan = (int2*)p.workspace;
+  a.plan = plan;
+  hipError_t e = launch_plan(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal, p.total_tokens,
+                             /*kind=*/0, a.group, cap, plan, stream);
+  if (e != hipSuccess) return e;
+  // workgroup r * Hq + h: list entry r, head h (the heads of one tile back to back)
+  hipLaunchKernelGGL(fwd_bf16_kernel<D>, dim3((unsigned)cap * (unsigned)p.num_q_heads), dim3(kThreads), 0, stream,
+                     a);
   return hipGetLastError();
 }
 

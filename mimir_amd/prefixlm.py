@@ -164,15 +164,18 @@ def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_
     q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
     out = torch.empty((T, hq, d), dtype=q.dtype, device=device)
     lse = torch.empty((hq, T), dtype=torch.float32, device=device)
+    max_all = _scalar(max_seqlen_all)
+    ws_bytes = int(_capi.load().mimir_prefixlm_fwd_workspace_bytes(T, n, max_all))
+    ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
     p = _capi.FwdParams(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
         pl.data_ptr(), cl.data_ptr(), cu.data_ptr(),
         q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
         out.stride(0), out.stride(1), lse.stride(0),
-        T, hq, hkv, d, n, _scalar(total_seqlen), _scalar(max_seqlen_all), int(bool(is_causal)),
-        _DTYPES[q.dtype], float(softmax_scale),
+        T, hq, hkv, d, n, _scalar(total_seqlen), max_all, int(bool(is_causal)),
+        _DTYPES[q.dtype], float(softmax_scale), ws.data_ptr(), ws_bytes,
     )
-    return p, out, lse, (q, k, v, pl, cl, cu)
+    return p, out, lse, (q, k, v, pl, cl, cu, ws)
 
 
 def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
@@ -207,7 +210,7 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
     dq = torch.empty((T, hq, d), dtype=q.dtype, device=device)
     dk = torch.empty((T, hkv, d), dtype=q.dtype, device=device)
     dv = torch.empty((T, hkv, d), dtype=q.dtype, device=device)
-    ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_bytes(T, hq))
+    ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_bytes(T, hq, n, _scalar(max_seqlen_all)))
     ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
     p = _capi.BwdParams(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(), lse.data_ptr(),

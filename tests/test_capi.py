@@ -50,8 +50,12 @@ def test_abi_version(lib):
 
 
 def test_workspace_bytes(lib):
-    assert lib.mimir_prefixlm_bwd_workspace_bytes(16384, 16) == 2 * 16384 * 16 * 4
-    assert lib.mimir_prefixlm_bwd_workspace_bytes(0, 16) == 0
+    # tile lists: one int32 pair per 128-row tile, min(numseqs * ceil(max_len / 128), ceil(T / 128) + numseqs)
+    assert lib.mimir_prefixlm_fwd_workspace_bytes(16384, 8, 2048) == 8 * 16 * 8
+    assert lib.mimir_prefixlm_fwd_workspace_bytes(16384, 1000, 4096) == (128 + 1000) * 8
+    assert lib.mimir_prefixlm_fwd_workspace_bytes(0, 8, 2048) == 0
+    assert lib.mimir_prefixlm_bwd_workspace_bytes(16384, 16, 8, 2048) == 2 * 16384 * 16 * 4 + 2 * 8 * 16 * 8
+    assert lib.mimir_prefixlm_bwd_workspace_bytes(0, 16, 8, 2048) == 0
 
 
 def _c_layout(struct_name, fields):
