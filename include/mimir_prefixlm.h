@@ -147,7 +147,7 @@ int mimir_prefixlm_bwd(const MimirPrefixLMBwdParams* params, void* stream);
  * independent of each other.  No reference counterpart: the reference exposes
  * the backward only through autograd (flash_attention_prefixlm_v2.py:270-283). */
 enum MimirBwdStage {
-  MIMIR_BWD_STAGE_DELTA = 1, /* delta = rowsum(O * dO) and lse * log2(e) into the workspace */
+  MIMIR_BWD_STAGE_DELTA = 1, /* delta = rowsum(O * dO), lse * log2(e) and the tile work lists into the workspace */
   MIMIR_BWD_STAGE_DKDV = 2,  /* dK, dV for every key row inside a sequence */
   MIMIR_BWD_STAGE_DQ = 4,    /* dQ for every active query row */
   MIMIR_BWD_STAGE_FILL = 8,  /* zero dQ / dK / dV rows outside every sequence */
@@ -155,9 +155,9 @@ enum MimirBwdStage {
 };
 int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* params, int stages, void* stream);
 
-/* Bytes of device workspace the backward needs: float32 delta = rowsum(O * dO) [Hq, T]
- * and float32 lse * log2(e) [Hq, T], both written by the DELTA stage, then the
- * tile work lists of the DQ and DKDV stages (each written by its stage). */
+/* Bytes of device workspace the backward needs: float32 delta = rowsum(O * dO) [Hq, T],
+ * float32 lse * log2(e) [Hq, T], then the tile work lists of the DQ and DKDV
+ * stages; the DELTA stage writes all four, DQ and DKDV read them. */
 size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads, int32_t numseqs,
                                           int32_t max_seqlen_all);
 

@@ -45,7 +45,7 @@ SOURCES = [
     "prefixlm_bwd_dkdv_bf16.hip",
     "prefixlm_bwd_dkdv_pair_bf16.hip",
     "prefixlm_f32.hip",
-    "prefixlm_plan.hip",
+    "prefixlm_prologue.hip",
 ]
 
 

@@ -31,8 +31,8 @@ struct BwdArgs {
   int group;
   int total_seqlen;
   int is_causal;
-  int2* plan_q;      // workspace: query-tile work list (dQ stage)
-  int2* plan_k;      // workspace: key-tile work list (dK / dV stage)
+  int2* plan_q;      // workspace: query-tile work list (read by the dQ stage)
+  int2* plan_k;      // workspace: key-tile work list (read by the dK / dV stage)
   int plan_cap;      // entries of each list (plan_capacity)
   const int2* plan;  // the list the launched kernel reads
   float scale;

@@ -13,11 +13,13 @@
 //           The GQA reduction over the q-heads of one kv head happens in
 //           registers, so no kernel needs atomics and results are deterministic.
 //
-// This file holds the delta kernel and the orchestration; the dQ and dK/dV
-// kernels live in prefixlm_bwd_dq_bf16.hip and prefixlm_bwd_dkdv_bf16.hip.  Both
-// tile loops stream their operand tiles with direct buffer-to-LDS loads into two
-// LDS stages (one barrier per tile).  Grids are ordered so that the heaviest
-// tiles of every sequence are dispatched first.
+// This file holds the orchestration.  The delta rows (with lse * log2(e)) and
+// both tile work lists come from the prologue launch (prefixlm_prologue.hip) of
+// the DELTA stage; the dQ kernel lives in prefixlm_bwd_dq_bf16.hip, the dK/dV
+// kernels in prefixlm_bwd_dkdv_pair_bf16.hip (head_dim 128) and
+// prefixlm_bwd_dkdv_bf16.hip (head_dim 64).  The tile loops stream their operand
+// tiles with direct buffer-to-LDS loads into multi-stage LDS rings, and every
+// workgroup takes its tile from a heaviest-first work list.
 //
 // Math: dV = P^T dO, dP = dO V^T, delta = rowsum(dO * O), dS = P (dP - delta) * scale,
 // dQ = dS K, dK = dS^T Q  (flash_attention_prefixlm_mps.py:1601-1675), with the GQA
@@ -27,37 +29,8 @@
 namespace {
 using namespace mimir;
 
-// ---------------------------------------------------------------------------
-// delta = rowsum(O * dO), one (token, head) row per D/8 lanes; the same pass
-// stores lse * log2(e), so the tile loops form P = exp2(S * scale * log2(e) - lse2)
-// with one FMA per score.
-// ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256) void delta_kernel(const BwdArgs a) {
-  constexpr int LPR = D / 8;  // lanes per row
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t row = gid / LPR;  // row = t * Hq + h
-  const int c = (int)(gid % LPR);
-  const bool valid = row < (int64_t)a.T * a.Hq;
-  const int t = valid ? (int)(row / a.Hq) : 0;
-  const int h = valid ? (int)(row % a.Hq) : 0;
-  float acc = 0.f;
-  if (valid) {
-    const bf16x8 ov = *(const bf16x8*)&a.o[(int64_t)t * a.o_st + (int64_t)h * a.o_sh + c * 8];
-    const bf16x8 dv = *(const bf16x8*)&a.dout[(int64_t)t * a.do_st + (int64_t)h * a.do_sh + c * 8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (float)ov[e] * (float)dv[e];
-  }
-#pragma unroll
-  for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (valid && c == 0) {
-    a.delta[(int64_t)h * a.T + t] = acc;
-    a.lse2[(int64_t)h * a.T + t] = a.lse[(int64_t)h * a.lse_sh + t] * kLog2e;
-  }
-}
-
-template <int D>
-hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages) {
+hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t stream, int stages) {
   BwdArgs a;
   a.q = (const bf16_t*)p.q;
   a.k = (const bf16_t*)p.k;
@@ -94,12 +67,19 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stage
   a.scale = p.softmax_scale;
   a.scale_log2 = p.softmax_scale * kLog2e;
 
-  const int64_t rows = (int64_t)p.total_tokens * p.num_q_heads;
-  if (rows > 0 && (stages & MIMIR_BWD_STAGE_DELTA)) {
-    const int64_t threads = rows * (D / 8);
-    hipLaunchKernelGGL(delta_kernel<D>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);
+  if (stages & MIMIR_BWD_STAGE_DELTA) {
+    DeltaArgs& d = pro.delta;
+    d.o = a.o; d.dout = a.dout; d.lse = a.lse; d.delta = a.delta; d.lse2 = a.lse2;
+    d.o_st = a.o_st; d.o_sh = a.o_sh; d.do_st = a.do_st; d.do_sh = a.do_sh; d.lse_sh = a.lse_sh;
+    d.T = a.T; d.Hq = a.Hq; d.D = D;
+    pro.has_delta = 1;
+    // both tile lists: the dK/dV stage reads kind 1, the dQ stage kind 0
+    pro.plan[pro.nplan++] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
+                                      p.total_tokens, /*kind=*/1, a.group, a.plan_cap, a.plan_k);
+    pro.plan[pro.nplan++] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
+                                      p.total_tokens, /*kind=*/0, a.group, a.plan_cap, a.plan_q);
   }
-  hipError_t e = hipGetLastError();
+  hipError_t e = launch_prologue(pro, stream);
   if (e != hipSuccess) return e;
   if (stages & MIMIR_BWD_STAGE_DKDV) {
     e = D == 128 ? launch_bwd_dkdv_pair_bf16(a, p.numseqs, p.max_seqlen_all, stream)
@@ -115,10 +95,10 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stage
 
 }  // namespace
 
-hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages) {
+hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t stream, int stages) {
   switch (p.head_dim) {
-    case 64: return launch<64>(p, stream, stages);
-    case 128: return launch<128>(p, stream, stages);
+    case 64: return launch<64>(p, pro, stream, stages);
+    case 128: return launch<128>(p, pro, stream, stages);
     default: return hipErrorInvalidValue;
   }
 }

@@ -260,10 +260,7 @@ hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream
   constexpr int kDkKeys = DkCfg<D>::kKeys, kDkWaves = DkCfg<D>::kWaves;
   static_assert(kDkKeys == kPlanTile, "work-list tiles are the dK / dV key tiles");
   if (numseqs <= 0 || a.plan_cap == 0) return hipSuccess;
-  hipError_t e = launch_plan(a.cu_seqlens, a.prefix_lens, numseqs, a.total_seqlen, a.is_causal, a.T, /*kind=*/1,
-                             a.group, a.plan_cap, a.plan_k, stream);
-  if (e != hipSuccess) return e;
-  a.plan = a.plan_k;
+  a.plan = a.plan_k;  // written by the DELTA stage's prologue
   // workgroup r * Hkv + h: list entry r, kv head h
   hipLaunchKernelGGL((dkdv_kernel<D>), dim3((unsigned)a.plan_cap * (unsigned)a.Hkv), dim3(kDkWaves * 64), 0,
                      stream, a);

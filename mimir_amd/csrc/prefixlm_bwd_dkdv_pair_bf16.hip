@@ -274,10 +274,7 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
 hipError_t launch_bwd_dkdv_pair_bf16(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   static_assert(kPairKeys == kPlanTile, "work-list tiles are the dK / dV key tiles");
   if (numseqs <= 0 || a.plan_cap == 0) return hipSuccess;
-  hipError_t e = launch_plan(a.cu_seqlens, a.prefix_lens, numseqs, a.total_seqlen, a.is_causal, a.T, /*kind=*/1,
-                             a.group, a.plan_cap, a.plan_k, stream);
-  if (e != hipSuccess) return e;
-  a.plan = a.plan_k;
+  a.plan = a.plan_k;  // written by the DELTA stage's prologue
   // workgroup r * Hkv + h: list entry r, kv head h
   hipLaunchKernelGGL(dkdv_pair_kernel, dim3((unsigned)a.plan_cap * (unsigned)a.Hkv), dim3(kPairWaves * 64), 0,
                      stream, a);

@@ -180,10 +180,7 @@ template <int D>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   static_assert(kBlockQ == kPlanTile, "work-list tiles are the dQ query tiles");
   if (numseqs <= 0 || a.plan_cap == 0) return hipSuccess;
-  hipError_t e = launch_plan(a.cu_seqlens, a.prefix_lens, numseqs, a.total_seqlen, a.is_causal, a.T, /*kind=*/0,
-                             a.group, a.plan_cap, a.plan_q, stream);
-  if (e != hipSuccess) return e;
-  a.plan = a.plan_q;
+  a.plan = a.plan_q;  // written by the DELTA stage's prologue
   // workgroup r * Hq + h: list entry r, head h
   hipLaunchKernelGGL(dq_kernel<D>, dim3((unsigned)a.plan_cap * (unsigned)a.Hq), dim3(kThreads), 0, stream, a);
   return hipGetLastError();

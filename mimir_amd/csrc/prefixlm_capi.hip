@@ -1,5 +1,5 @@
-// C ABI of libmimir_prefixlm.so: argument validation, dtype / head_dim dispatch,
-// padding-row fills and the metadata check.  Declarations and the contract live
+// C ABI of libmimir_prefixlm.so: argument validation, dtype / head_dim dispatch
+// and the metadata check.  Declarations and the contract live
 // in include/mimir_prefixlm.h.
 #include <cmath>
 #include <cstdio>
@@ -19,54 +19,6 @@ int fail(int code, const std::string& msg) {
 int hip_status(hipError_t e, const char* what) {
   if (e == hipSuccess) return MIMIR_OK;
   return fail(MIMIR_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
-}
-
-// Rows that belong to no sequence, or lie at/after total_seqlen, are outputs of
-// the operator too: O = 0, lse = -inf, dQ = 0 (flash_attention_prefixlm_dense.py:43,79-80).
-// dK/dV rows outside every sequence are 0; key rows inside a sequence are written
-// by the dK/dV kernel even at/after total_seqlen, since they remain keys there.
-constexpr int kFillRows = 16;
-
-struct FillArgs {
-  void* x;            // [T, H, D] of elem_bytes
-  int64_t st, sh;     // strides in elements
-  float* lse;         // optional [H, T]
-  int64_t lse_sh;
-  const int32_t* cu_seqlens;
-  int numseqs, total_seqlen, T, H, row_bytes, elem_bytes;
-};
-
-__global__ __launch_bounds__(256) void fill_rows_kernel(const FillArgs a) {
-  const int t0 = blockIdx.x * kFillRows;
-  const int first = a.numseqs > 0 ? a.cu_seqlens[0] : a.T;
-  int last = a.numseqs > 0 ? a.cu_seqlens[a.numseqs] : 0;
-  if (last > a.total_seqlen) last = a.total_seqlen;
-  // inactive rows: t < first or t >= last
-  const int t1 = min(t0 + kFillRows, a.T);
-  if (t0 >= first && t1 <= last) return;
-  const int chunks = a.row_bytes / 4;  // row_bytes is a multiple of 4
-  for (int i = threadIdx.x; i < kFillRows * a.H * chunks; i += blockDim.x) {
-    const int tt = i / (a.H * chunks);
-    const int rem = i % (a.H * chunks);
-    const int h = rem / chunks, c = rem % chunks;
-    const int t = t0 + tt;
-    if (t >= a.T || (t >= first && t < last)) continue;
-    char* row = (char*)a.x + ((int64_t)t * a.st + (int64_t)h * a.sh) * a.elem_bytes;
-    ((uint32_t*)row)[c] = 0u;
-    if (c == 0 && a.lse != nullptr) a.lse[(int64_t)h * a.lse_sh + t] = -INFINITY;
-  }
-}
-
-hipError_t launch_fill(void* x, int64_t st, int64_t sh, float* lse, int64_t lse_sh, const int32_t* cu,
-                       int numseqs, int total_seqlen, int T, int H, int D, int elem_bytes,
-                       hipStream_t stream) {
-  if (T <= 0 || H <= 0) return hipSuccess;
-  FillArgs a;
-  a.x = x; a.st = st; a.sh = sh; a.lse = lse; a.lse_sh = lse_sh; a.cu_seqlens = cu;
-  a.numseqs = numseqs; a.total_seqlen = total_seqlen; a.T = T; a.H = H;
-  a.row_bytes = D * elem_bytes; a.elem_bytes = elem_bytes;
-  hipLaunchKernelGGL(fill_rows_kernel, dim3((T + kFillRows - 1) / kFillRows), dim3(256), 0, stream, a);
-  return hipGetLastError();
 }
 
 __global__ __launch_bounds__(256) void check_metadata_kernel(const int32_t* prefix_lens,
@@ -191,11 +143,18 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* p, void* stream_) {
   if (need > 0 && (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace)))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +
                                                 std::to_string(need) + " bytes");
-  hipError_t e = dt == MIMIR_DTYPE_BFLOAT16 ? mimir_launch_fwd_bf16(*p, stream) : mimir_launch_fwd_f32(*p, stream);
-  if ((rc = hip_status(e, "forward launch"))) return rc;
-  e = launch_fill(p->out, p->out_stride_token, p->out_stride_head, p->lse, p->lse_stride_head, p->cu_seqlens,
-                  p->numseqs, p->total_seqlen, p->total_tokens, p->num_q_heads, D, elem_bytes_of(dt), stream);
-  return hip_status(e, "forward padding fill");
+  mimir::Prologue pro;
+  pro.fill[pro.nfill++] = mimir::fill_args(p->out, p->out_stride_token, p->out_stride_head, p->lse,
+                                           p->lse_stride_head, p->cu_seqlens, p->numseqs, p->total_seqlen,
+                                           p->total_tokens, p->num_q_heads, D, elem_bytes_of(dt));
+  hipError_t e;
+  if (dt == MIMIR_DTYPE_BFLOAT16) {
+    e = mimir_launch_fwd_bf16(*p, pro, stream);
+  } else {
+    e = mimir::launch_prologue(pro, stream);
+    if (e == hipSuccess) e = mimir_launch_fwd_f32(*p, stream);
+  }
+  return hip_status(e, "forward launch");
 }
 
 int mimir_prefixlm_bwd(const MimirPrefixLMBwdParams* p, void* stream) {
@@ -230,20 +189,25 @@ int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* p, int stages, void*
   if (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +
                                                 std::to_string(need) + " bytes");
-  hipError_t e = dt == MIMIR_DTYPE_BFLOAT16 ? mimir_launch_bwd_bf16(*p, stream, stages)
-                                            : mimir_launch_bwd_f32(*p, stream, stages);
-  if ((rc = hip_status(e, "backward launch"))) return rc;
-  if (!(stages & MIMIR_BWD_STAGE_FILL)) return MIMIR_OK;
-  const int es = elem_bytes_of(dt);
-  e = launch_fill(p->dq, p->dq_stride_token, p->dq_stride_head, nullptr, 0, p->cu_seqlens, p->numseqs,
-                  p->total_seqlen, p->total_tokens, p->num_q_heads, D, es, stream);
-  if ((rc = hip_status(e, "dq padding fill"))) return rc;
-  e = launch_fill(p->dk, p->dk_stride_token, p->dk_stride_head, nullptr, 0, p->cu_seqlens, p->numseqs,
-                  p->total_tokens, p->total_tokens, p->num_kv_heads, D, es, stream);
-  if ((rc = hip_status(e, "dk padding fill"))) return rc;
-  e = launch_fill(p->dv, p->dv_stride_token, p->dv_stride_head, nullptr, 0, p->cu_seqlens, p->numseqs,
-                  p->total_tokens, p->total_tokens, p->num_kv_heads, D, es, stream);
-  return hip_status(e, "dv padding fill");
+  mimir::Prologue pro;
+  if (stages & MIMIR_BWD_STAGE_FILL) {
+    // dQ rows at/after total_seqlen are zero; dK / dV rows inside a sequence stay keys there.
+    const int es = elem_bytes_of(dt);
+    pro.fill[pro.nfill++] = mimir::fill_args(p->dq, p->dq_stride_token, p->dq_stride_head, nullptr, 0, p->cu_seqlens,
+                                             p->numseqs, p->total_seqlen, p->total_tokens, p->num_q_heads, D, es);
+    pro.fill[pro.nfill++] = mimir::fill_args(p->dk, p->dk_stride_token, p->dk_stride_head, nullptr, 0, p->cu_seqlens,
+                                             p->numseqs, p->total_tokens, p->total_tokens, p->num_kv_heads, D, es);
+    pro.fill[pro.nfill++] = mimir::fill_args(p->dv, p->dv_stride_token, p->dv_stride_head, nullptr, 0, p->cu_seqlens,
+                                             p->numseqs, p->total_tokens, p->total_tokens, p->num_kv_heads, D, es);
+  }
+  hipError_t e;
+  if (dt == MIMIR_DTYPE_BFLOAT16) {
+    e = mimir_launch_bwd_bf16(*p, pro, stream, stages);
+  } else {
+    e = mimir::launch_prologue(pro, stream);
+    if (e == hipSuccess) e = mimir_launch_bwd_f32(*p, stream, stages);
+  }
+  return hip_status(e, "backward launch");
 }
 
 }  // extern "C"

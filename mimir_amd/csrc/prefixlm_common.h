@@ -269,26 +269,69 @@ __device__ __forceinline__ void stage_barrier() {
 }  // namespace mimir
 
 namespace mimir {
-// Tile work lists (prefixlm_plan.hip).  kind 0: 128-row query tiles (forward,
-// dQ); kind 1: 128-key tiles (dK / dV).  The list of capacity plan_capacity()
-// int2 (sequence, tile) entries is sorted by cost, descending, and padded with
+// The per-call work in front of the tile loops (prefixlm_prologue.hip), run as
+// one launch: tile work lists, the backward's delta rows, padding-row fills.
+//
+// Tile work lists: kind 0 holds 128-row query tiles (forward, dQ), kind 1
+// 128-key tiles (dK / dV).  A list of capacity plan_capacity() int2
+// (sequence, tile) entries is sorted by cost, descending, and padded with
 // (-1, -1); workgroup r * H + h of a consumer takes entry r for head h.
 constexpr int kPlanTile = 128;
 int plan_capacity(int total_tokens, int numseqs, int max_seqlen_all);
-hipError_t launch_plan(const int32_t* cu_seqlens, const int32_t* prefix_lens, int numseqs, int total_seqlen,
-                       int is_causal, int total_tokens, int kind, int group, int cap, int2* items,
-                       hipStream_t stream);
+
+struct PlanArgs {
+  const int32_t* cu_seqlens;
+  const int32_t* prefix_lens;
+  int numseqs, total_seqlen, is_causal, T, kind, group, cap;
+  int2* items;
+};
+
+// delta[h, t] = sum_d O[t, h, d] * dO[t, h, d] and lse2[h, t] = lse[h, t] * log2(e), bf16 O / dO.
+struct DeltaArgs {
+  const bf16_t* o;
+  const bf16_t* dout;
+  const float* lse;
+  float* delta;
+  float* lse2;
+  int64_t o_st, o_sh, do_st, do_sh, lse_sh;
+  int T, Hq, D;
+};
+
+// Zero the rows of one [T, H, D] tensor (and lse = -inf if non-NULL) that lie
+// outside [cu_seqlens[0], min(cu_seqlens[numseqs], total_seqlen)).
+struct FillArgs {
+  void* x;         // [T, H, D] of elem_bytes
+  int64_t st, sh;  // strides in elements
+  float* lse;      // optional [H, T]
+  int64_t lse_sh;
+  const int32_t* cu_seqlens;
+  int numseqs, total_seqlen, T, H, row_bytes, elem_bytes;
+};
+
+struct Prologue {
+  PlanArgs plan[2];
+  int nplan = 0;
+  DeltaArgs delta;
+  int has_delta = 0;
+  FillArgs fill[3];  // targets of one launch share T
+  int nfill = 0;
+};
+
+PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int numseqs, int total_seqlen,
+                   int is_causal, int total_tokens, int kind, int group, int cap, int2* items);
+FillArgs fill_args(void* x, int64_t st, int64_t sh, float* lse, int64_t lse_sh, const int32_t* cu, int numseqs,
+                   int total_seqlen, int T, int H, int D, int elem_bytes);
+hipError_t launch_prologue(const Prologue& pro, hipStream_t stream);
 }  // namespace mimir
 
-// Internal launchers (implemented per kernel file, dispatched from prefixlm_capi.cpp).
-hipError_t mimir_launch_fwd_bf16(const MimirPrefixLMFwdParams& p, hipStream_t stream);
-hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages);
+// Internal launchers (implemented per kernel file, dispatched from prefixlm_capi.hip).
+// The bf16 launchers add their tile lists (and the backward its delta rows) to
+// `pro`, which holds the caller's padding fills, and launch it before their
+// tile kernels.
+hipError_t mimir_launch_fwd_bf16(const MimirPrefixLMFwdParams& p, mimir::Prologue pro, hipStream_t stream);
+hipError_t mimir_launch_bwd_bf16(const MimirPrefixLMBwdParams& p, mimir::Prologue pro, hipStream_t stream,
+                                 int stages);
 hipError_t mimir_launch_fwd_f32(const MimirPrefixLMFwdParams& p, hipStream_t stream);
 hipError_t mimir_launch_bwd_f32(const MimirPrefixLMBwdParams& p, hipStream_t stream, int stages);
-hipError_t mimir_launch_fill_fwd_padding(const MimirPrefixLMFwdParams& p, hipStream_t stream);
-hipError_t mimir_launch_fill_bwd_padding(const MimirPrefixLMBwdParams& p, hipStream_t stream);
-hipError_t mimir_launch_check_metadata(const int32_t* prefix_lens, const int32_t* causal_lens,
-                                       const int32_t* cu_seqlens, int32_t numseqs, int32_t* bad_seq,
-                                       hipStream_t stream);
 bool mimir_bf16_head_dim_supported(int d);
 bool mimir_f32_head_dim_supported(int d);

@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
 }
 
 template <int D>
-hipError_t launch(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
+hipError_t launch(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t stream) {
   FwdArgs a;
   a.q = (const bf16_t*)p.q;
   a.k = (const bf16_t*)p.k;
@@ -272,12 +272,13 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
   a.scale_log2 = p.softmax_scale * kLog2e;
   static_assert(kBlockM == kPlanTile, "work-list tiles are the forward's query tiles");
   const int cap = plan_capacity(p.total_tokens, p.numseqs, p.max_seqlen_all);
-  if (cap == 0) return hipSuccess;
   int2* plan = (int2*)p.workspace;
   a.plan = plan;
-  hipError_t e = launch_plan(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal, p.total_tokens,
-                             /*kind=*/0, a.group, cap, plan, stream);
-  if (e != hipSuccess) return e;
+  if (cap > 0)
+    pro.plan[pro.nplan++] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
+                                      p.total_tokens, /*kind=*/0, a.group, cap, plan);
+  hipError_t e = launch_prologue(pro, stream);
+  if (e != hipSuccess || cap == 0) return e;
   // workgroup r * Hq + h: list entry r, head h (the heads of one tile back to back)
   hipLaunchKernelGGL(fwd_bf16_kernel<D>, dim3((unsigned)cap * (unsigned)p.num_q_heads), dim3(kThreads), 0, stream,
                      a);
@@ -288,10 +289,10 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
 
 bool mimir_bf16_head_dim_supported(int d) { return d == 64 || d == 128; }
 
-hipError_t mimir_launch_fwd_bf16(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
+hipError_t mimir_launch_fwd_bf16(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t stream) {
   switch (p.head_dim) {
-    case 64: return launch<64>(p, stream);
-    case 128: return launch<128>(p, stream);
+    case 64: return launch<64>(p, pro, stream);
+    case 128: return launch<128>(p, pro, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -1,0 +1,292 @@
+// The small per-call work in front of the tile loops, in one launch: the tile
+// work lists, the backward's delta / lse * log2(e) rows and the padding-row
+// fills.  Separate launches cost a few microseconds each of mostly idle GPU;
+// here the workgroups of the three jobs share one grid and run side by side.
+//
+//   workgroups [0, nplan)               one tile work list each
+//   then [0, delta_blocks)               delta = rowsum(O * dO), lse * log2(e)
+//   then nfill x [0, fill_blocks)        zero rows outside every sequence
+//
+// Tile work lists: which (sequence, 128-row tile) each workgroup of the forward,
+// dQ and dK/dV kernels takes, heaviest first.  Dispatching (column, tile row)
+// rectangles row by row only approximates heaviest-first: on batches of a few
+// 2k sequences the last workgroups to start were still large and the kernels
+// ended on long tails.  One workgroup computes every item's cost from the
+// metadata on the device (no host copy of cu_seqlens / prefix_lens),
+// counting-sorts the items by cost, descending, into the caller's workspace and
+// pads the list with (-1, -1).  Workgroup r * H + h of the consumer takes list
+// entry r for head h: the H heads of one item run back to back and the dispatch
+// order is longest-processing-time first.  The order inside one cost bucket
+// follows LDS atomics and may differ from call to call; every item writes its
+// own outputs, so results do not.
+//
+// Costs, in 64-row tiles of the inner loop:
+//   query tiles (forward, dQ):  key tiles up to kend of the tile's last row,
+//                               ceil(max(p, min(m0 + 128, nq)) / 64)
+//   key tiles (dK / dV):        G * query tiles from qstart(first key),
+//                               G * ceil((nq - qstart(kb0)) / 64), 0 if none
+//
+// Padding rows: rows that belong to no sequence, or lie at/after total_seqlen,
+// are outputs of the operator too: O = 0, lse = -inf, dQ = 0
+// (flash_attention_prefixlm_dense.py:43,79-80).  dK/dV rows outside every
+// sequence are 0; key rows inside a sequence are written by the dK/dV kernel
+// even at/after total_seqlen, since they remain keys there.  The fills touch
+// only rows the tile kernels never write, so they may run before them.
+#include "prefixlm_common.h"
+
+namespace mimir {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kPlanBuckets = 4096;  // costs above kPlanBuckets - 1 share the last bucket
+constexpr int kBucketsPerThread = kPlanBuckets / kThreads;
+constexpr int kFillRows = 16;
+
+struct PrologueArgs {
+  PlanArgs plan[2];
+  DeltaArgs delta;
+  FillArgs fill[3];
+  int nplan, delta_blocks, nfill, fill_blocks;
+};
+
+// Exclusive prefix sum of v over the workgroup; `total` receives the sum.
+__device__ int block_exclusive_scan(int v, int* wave_sums, int& total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) wave_sums[w] = x;
+  __syncthreads();
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    const int s = wave_sums[i];
+    before += i < w ? s : 0;
+    total += s;
+  }
+  __syncthreads();  // wave_sums is reused by the next scan
+  return before + x - v;
+}
+
+__device__ __forceinline__ int item_cost(int p, int nq, int kind, int group, int t) {
+  int c;
+  if (kind == 0) {
+    const int kend = max(p, min(t * kPlanTile + kPlanTile, nq));
+    c = (kend + 63) / 64;
+  } else {
+    const int q0 = qstart_of(p, t * kPlanTile);
+    c = nq > q0 ? group * ((nq - q0 + 63) / 64) : 0;
+  }
+  return min(c, kPlanBuckets - 1);
+}
+
+struct PlanSmem {
+  int hist[kPlanBuckets];
+  int first_item[kThreads];  // per sequence of the current chunk
+  int p[kThreads], nq[kThreads];
+  int wave_sums[kWaves];
+};
+
+// Visits every (sequence, tile) item, 256 sequences at a time: a scan of the
+// tile counts gives each sequence its first item, then the items are dealt to
+// the threads one each, so a single long sequence is spread over the workgroup
+// too.  Pass 1 counts items per cost bucket, pass 2 (kScatter) writes them.
+template <bool kScatter>
+__device__ void walk_items(const PlanArgs& a, PlanSmem& sm) {
+  for (int base = 0; base < a.numseqs; base += kThreads) {
+    const int s = base + (int)threadIdx.x;
+    int nt = 0, p = 0, nq = 0;
+    if (s < a.numseqs) {
+      const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+      nt = ((a.kind == 0 ? g.nq : g.n) + kPlanTile - 1) / kPlanTile;
+      p = g.p;
+      nq = g.nq;
+    }
+    int total;
+    const int first = block_exclusive_scan(nt, sm.wave_sums, total);
+    sm.first_item[threadIdx.x] = first;
+    sm.p[threadIdx.x] = p;
+    sm.nq[threadIdx.x] = nq;
+    __syncthreads();
+    for (int i = threadIdx.x; i < total; i += kThreads) {
+      // the last sequence of the chunk whose first item is <= i owns item i
+      int j = 0;
+#pragma unroll
+      for (int step = kThreads / 2; step > 0; step >>= 1)
+        if (sm.first_item[j + step] <= i) j += step;
+      const int t = i - sm.first_item[j];
+      const int c = item_cost(sm.p[j], sm.nq[j], a.kind, a.group, t);
+      if constexpr (kScatter) {
+        const int pos = atomicAdd(&sm.hist[c], 1);
+        if (pos < a.cap) a.items[pos] = make_int2(base + j, t);
+      } else {
+        atomicAdd(&sm.hist[c], 1);
+      }
+    }
+    __syncthreads();  // the chunk arrays are rewritten by the next chunk
+  }
+}
+
+__device__ void plan_block(const PlanArgs& a) {
+  __shared__ PlanSmem sm;
+  for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
+  __syncthreads();
+  walk_items<false>(a, sm);
+  // Bucket starts in descending cost order: bucket c starts after all items of
+  // cost > c.  Thread i owns buckets kPlanBuckets-1-16i down to kPlanBuckets-16-16i.
+  int local = 0;
+#pragma unroll
+  for (int j = 0; j < kBucketsPerThread; ++j) local += sm.hist[kPlanBuckets - 1 - (kBucketsPerThread * threadIdx.x + j)];
+  int total;
+  int run = block_exclusive_scan(local, sm.wave_sums, total);
+#pragma unroll
+  for (int j = 0; j < kBucketsPerThread; ++j) {
+    const int b = kPlanBuckets - 1 - (kBucketsPerThread * threadIdx.x + j);
+    const int h = sm.hist[b];
+    sm.hist[b] = run;  // becomes the next free position of bucket b
+    run += h;
+  }
+  __syncthreads();
+  walk_items<true>(a, sm);
+  for (int i = total + threadIdx.x; i < a.cap; i += kThreads) a.items[i] = make_int2(-1, -1);
+}
+
+// delta = rowsum(O * dO) and lse * log2(e) for 256 / (D / 8) (token, head) rows;
+// the tile loops then form P = exp2(S * scale * log2(e) - lse2) with one FMA.
+template <int D>
+__device__ void delta_block(const DeltaArgs& a, int b) {
+  constexpr int LPR = D / 8;  // lanes per row
+  const int64_t gid = (int64_t)b * kThreads + threadIdx.x;
+  const int64_t row = gid / LPR;  // row = t * Hq + h
+  const int c = (int)(gid % LPR);
+  const bool valid = row < (int64_t)a.T * a.Hq;
+  const int t = valid ? (int)(row / a.Hq) : 0;
+  const int h = valid ? (int)(row % a.Hq) : 0;
+  float acc = 0.f;
+  if (valid) {
+    const bf16x8 ov = *(const bf16x8*)&a.o[(int64_t)t * a.o_st + (int64_t)h * a.o_sh + c * 8];
+    const bf16x8 dv = *(const bf16x8*)&a.dout[(int64_t)t * a.do_st + (int64_t)h * a.do_sh + c * 8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += (float)ov[e] * (float)dv[e];
+  }
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (valid && c == 0) {
+    a.delta[(int64_t)h * a.T + t] = acc;
+    a.lse2[(int64_t)h * a.T + t] = a.lse[(int64_t)h * a.lse_sh + t] * kLog2e;
+  }
+}
+
+// Zeroes the padding rows among packed rows [16 b, 16 b + 16) of one tensor.
+__device__ void fill_block(const FillArgs& a, int b) {
+  const int t0 = b * kFillRows;
+  const int first = a.numseqs > 0 ? a.cu_seqlens[0] : a.T;
+  int last = a.numseqs > 0 ? a.cu_seqlens[a.numseqs] : 0;
+  if (last > a.total_seqlen) last = a.total_seqlen;
+  // inactive rows: t < first or t >= last
+  const int t1 = min(t0 + kFillRows, a.T);
+  if (t0 >= first && t1 <= last) return;
+  const int chunks = a.row_bytes / 4;  // row_bytes is a multiple of 4
+  for (int i = threadIdx.x; i < kFillRows * a.H * chunks; i += kThreads) {
+    const int tt = i / (a.H * chunks);
+    const int rem = i % (a.H * chunks);
+    const int h = rem / chunks, c = rem % chunks;
+    const int t = t0 + tt;
+    if (t >= a.T || (t >= first && t < last)) continue;
+    char* row = (char*)a.x + ((int64_t)t * a.st + (int64_t)h * a.sh) * a.elem_bytes;
+    ((uint32_t*)row)[c] = 0u;
+    if (c == 0 && a.lse != nullptr) a.lse[(int64_t)h * a.lse_sh + t] = -INFINITY;
+  }
+}
+
+template <int kDeltaD>  // 0: no delta rows
+__global__ __launch_bounds__(kThreads) void prologue_kernel(const PrologueArgs a) {
+  int b = blockIdx.x;
+  if (b < a.nplan) {
+    plan_block(b == 0 ? a.plan[0] : a.plan[1]);
+    return;
+  }
+  b -= a.nplan;
+  if constexpr (kDeltaD > 0) {
+    if (b < a.delta_blocks) {
+      delta_block<kDeltaD>(a.delta, b);
+      return;
+    }
+    b -= a.delta_blocks;
+  }
+  const int target = b / a.fill_blocks;
+  fill_block(a.fill[target], b - target * a.fill_blocks);
+}
+
+}  // namespace
+
+int plan_capacity(int total_tokens, int numseqs, int max_seqlen_all) {
+  if (numseqs <= 0 || max_seqlen_all <= 0) return 0;
+  const int64_t rect = (int64_t)numseqs * ((max_seqlen_all + kPlanTile - 1) / kPlanTile);
+  const int64_t bound = (int64_t)(total_tokens + kPlanTile - 1) / kPlanTile + numseqs;
+  return (int)(rect < bound ? rect : bound);
+}
+
+PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int numseqs, int total_seqlen,
+                   int is_causal, int total_tokens, int kind, int group, int cap, int2* items) {
+  PlanArgs a;
+  a.cu_seqlens = cu_seqlens;
+  a.prefix_lens = prefix_lens;
+  a.numseqs = numseqs;
+  a.total_seqlen = total_seqlen;
+  a.is_causal = is_causal;
+  a.T = total_tokens;
+  a.kind = kind;
+  a.group = group;
+  a.cap = cap;
+  a.items = items;
+  return a;
+}
+
+FillArgs fill_args(void* x, int64_t st, int64_t sh, float* lse, int64_t lse_sh, const int32_t* cu, int numseqs,
+                   int total_seqlen, int T, int H, int D, int elem_bytes) {
+  FillArgs a;
+  a.x = x; a.st = st; a.sh = sh; a.lse = lse; a.lse_sh = lse_sh; a.cu_seqlens = cu;
+  a.numseqs = numseqs; a.total_seqlen = total_seqlen; a.T = T; a.H = H;
+  a.row_bytes = D * elem_bytes; a.elem_bytes = elem_bytes;
+  return a;
+}
+
+hipError_t launch_prologue(const Prologue& pro, hipStream_t stream) {
+  PrologueArgs a;
+  a.nplan = 0;
+  for (int i = 0; i < pro.nplan; ++i)
+    if (pro.plan[i].cap > 0) a.plan[a.nplan++] = pro.plan[i];
+  a.delta = pro.delta;
+  a.delta_blocks = 0;
+  int delta_d = 0;
+  if (pro.has_delta && (int64_t)pro.delta.T * pro.delta.Hq > 0) {
+    delta_d = pro.delta.D;
+    const int64_t threads = (int64_t)pro.delta.T * pro.delta.Hq * (delta_d / 8);
+    a.delta_blocks = (int)((threads + kThreads - 1) / kThreads);
+  }
+  a.nfill = 0;
+  a.fill_blocks = 0;
+  for (int i = 0; i < pro.nfill; ++i)
+    if (pro.fill[i].T > 0 && pro.fill[i].H > 0) {
+      a.fill[a.nfill++] = pro.fill[i];
+      a.fill_blocks = (pro.fill[i].T + kFillRows - 1) / kFillRows;  // every target has the same T
+    }
+  const int64_t blocks = (int64_t)a.nplan + a.delta_blocks + (int64_t)a.nfill * a.fill_blocks;
+  if (blocks == 0) return hipSuccess;
+  const dim3 grid((unsigned)blocks), block(kThreads);
+  switch (delta_d) {
+    case 0: hipLaunchKernelGGL(prologue_kernel<0>, grid, block, 0, stream, a); break;
+    case 64: hipLaunchKernelGGL(prologue_kernel<64>, grid, block, 0, stream, a); break;
+    case 128: hipLaunchKernelGGL(prologue_kernel<128>, grid, block, 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mimir
