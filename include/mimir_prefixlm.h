@@ -156,8 +156,11 @@ enum MimirBwdStage {
 int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* params, int stages, void* stream);
 
 /* Bytes of device workspace the backward needs: float32 delta = rowsum(O * dO) [Hq, T],
- * float32 lse * log2(e) [Hq, T], then the tile work lists of the DQ and DKDV
- * stages; the DELTA stage writes all four, DQ and DKDV read them. */
+ * float32 lse * log2(e) [Hq, T], the tile work lists of the DQ and DKDV stages,
+ * and for head_dim 128 the counters and float32 partial-sum slots of key tiles
+ * that the DKDV stage splits in two (at most 384 (tile, kv head) splits, 256 KiB
+ * each).  The DELTA stage writes the lists and zeroes the counters; DQ and DKDV
+ * read them, and DKDV leaves the counters at zero. */
 size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads, int32_t numseqs,
                                           int32_t max_seqlen_all);
 

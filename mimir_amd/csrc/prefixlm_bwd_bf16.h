@@ -32,9 +32,12 @@ struct BwdArgs {
   int total_seqlen;
   int is_causal;
   int2* plan_q;      // workspace: query-tile work list (read by the dQ stage)
-  int2* plan_k;      // workspace: key-tile work list (read by the dK / dV stage)
-  int plan_cap;      // entries of each list (plan_capacity)
-  const int2* plan;  // the list the launched kernel reads
+  int4* plan_k;      // workspace: key-tile work list (read by the dK / dV stage)
+  int cap_q, cap_k;  // entries of each list
+  const int2* plan;  // the query-tile list, for the dQ kernel
+  int* split_ctr;    // workspace: arrival counter per (pair, kv head)
+  int* queue;        // workspace: [0] next unit, [1] finished workgroups (dK / dV work queue)
+  float* split_buf;  // workspace: two kSplitSlotFloats slots per (pair, kv head)
   float scale;
   float scale_log2;
 };

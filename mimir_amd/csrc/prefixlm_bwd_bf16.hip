@@ -41,12 +41,18 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   a.dq = (bf16_t*)p.dq;
   a.dk = (bf16_t*)p.dk;
   a.dv = (bf16_t*)p.dv;
-  a.delta = (float*)p.workspace;
-  a.lse2 = (float*)p.workspace + (int64_t)p.num_q_heads * p.total_tokens;
-  a.plan_cap = plan_capacity(p.total_tokens, p.numseqs, p.max_seqlen_all);
-  a.plan_q = (int2*)((float*)p.workspace + 2 * (int64_t)p.num_q_heads * p.total_tokens);
-  a.plan_k = a.plan_q + a.plan_cap;
-  a.plan = nullptr;
+  const BwdWorkspace ws = bwd_workspace_layout(p.total_tokens, p.num_q_heads, p.numseqs, p.max_seqlen_all);
+  char* const wsb = (char*)p.workspace;
+  a.delta = (float*)(wsb + ws.delta);
+  a.lse2 = (float*)(wsb + ws.lse2);
+  a.plan_q = (int2*)(wsb + ws.plan_q);
+  a.plan_k = (int4*)(wsb + ws.plan_k);
+  a.cap_q = ws.cap_q;
+  a.cap_k = ws.cap_k;
+  a.plan = a.plan_q;
+  a.split_ctr = (int*)(wsb + ws.counters);
+  a.queue = a.split_ctr + ws.pair_heads;
+  a.split_buf = (float*)(wsb + ws.slots);
   a.prefix_lens = p.prefix_lens;
   a.cu_seqlens = p.cu_seqlens;
   a.q_st = p.q_stride_token; a.q_sh = p.q_stride_head;
@@ -74,10 +80,18 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
     d.T = a.T; d.Hq = a.Hq; d.D = D;
     pro.has_delta = 1;
     // both tile lists: the dK/dV stage reads kind 1, the dQ stage kind 0
+    PlanArgs pk = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal, p.total_tokens,
+                            /*kind=*/1, a.group, a.cap_k, a.plan_k);
+    if (D == 128 && ws.pair_heads >= a.Hkv) {  // the paired kernel (one workgroup per CU) adds split partials
+      pk.split_heads = a.Hkv;
+      pk.max_pairs = ws.pair_heads / a.Hkv;
+      pk.slots = device_cu_count();
+    }
+    pk.zero = a.split_ctr;  // split counters and the dK / dV work queue
+    pk.n_zero = ws.pair_heads + 2;
+    pro.plan[pro.nplan++] = pk;
     pro.plan[pro.nplan++] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
-                                      p.total_tokens, /*kind=*/1, a.group, a.plan_cap, a.plan_k);
-    pro.plan[pro.nplan++] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
-                                      p.total_tokens, /*kind=*/0, a.group, a.plan_cap, a.plan_q);
+                                      p.total_tokens, /*kind=*/0, a.group, a.cap_q, a.plan_q);
   }
   hipError_t e = launch_prologue(pro, stream);
   if (e != hipSuccess) return e;

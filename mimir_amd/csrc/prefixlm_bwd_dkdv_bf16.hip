@@ -12,7 +12,7 @@ namespace {
 // fragments come from the row-major LDS tiles via ds_read_b64_tr_b16.
 // The query range starts at qstart(first key) = (key < p ? 0 : key).
 // Workgroup r * Hkv + h takes kv head h of entry r of the key-tile work list
-// (prefixlm_plan.hip): the heaviest key tiles first.
+// (prefixlm_prologue.hip): the heaviest key tiles first.
 //
 // At head_dim 128 the K / V fragments and the dK / dV accumulators allow one
 // wave per SIMD, so LDS latency is hidden inside the wave: every operand
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   const int hi = lane >> 5;
   const int rank = blockIdx.x / a.Hkv;
   const int hk = blockIdx.x - rank * a.Hkv;
-  const int2 item = a.plan[rank];
+  const int4 item = a.plan_k[rank];  // never split for this kernel: part 0
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int ktile = item.y;
@@ -259,10 +259,9 @@ template <int D>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   constexpr int kDkKeys = DkCfg<D>::kKeys, kDkWaves = DkCfg<D>::kWaves;
   static_assert(kDkKeys == kPlanTile, "work-list tiles are the dK / dV key tiles");
-  if (numseqs <= 0 || a.plan_cap == 0) return hipSuccess;
-  a.plan = a.plan_k;  // written by the DELTA stage's prologue
+  if (numseqs <= 0 || a.cap_k == 0) return hipSuccess;
   // workgroup r * Hkv + h: list entry r, kv head h
-  hipLaunchKernelGGL((dkdv_kernel<D>), dim3((unsigned)a.plan_cap * (unsigned)a.Hkv), dim3(kDkWaves * 64), 0,
+  hipLaunchKernelGGL((dkdv_kernel<D>), dim3((unsigned)a.cap_k * (unsigned)a.Hkv), dim3(kDkWaves * 64), 0,
                      stream, a);
   return hipGetLastError();
 }

@@ -51,6 +51,9 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   __shared__ __attribute__((aligned(16))) bf16_t sV[2 * L::kElems];
   static_assert(64 * 64 * 4 <= L::kElems * 2, "one slice's partials fit one tile object");
 
+  __shared__ int unit_next;  // the workgroup's next work unit
+  __shared__ int later;      // split tiles: 1 if this half arrived second
+
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -58,14 +61,25 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   const int qh = wave >> 2;    // 32-query half of each tile
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-  const int rank = blockIdx.x / a.Hkv;
-  const int hk = blockIdx.x - rank * a.Hkv;
-  const int2 item = a.plan[rank];
-  if (item.x < 0) return;  // list padding
+  const Loader ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane), ldv(a.v_st, wave, lane);
+  const TileLanes<D> tl(lane);
+  const float c2 = a.scale_log2;
+  auto fetch_unit = [&]() {  // next work unit from the launch-wide queue
+    return (int)gridDim.x + __hip_atomic_fetch_add(&a.queue[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+
+  // One work unit: kv head hk of key-tile list entry `item`.  Thread 0 fetches
+  // the workgroup's next unit into `nxt` as soon as the tile loop is done, so
+  // the queue hands out units in list order to whichever workgroup frees up.
+  auto run_unit = [&](const int4 item, const int hk, int& nxt) {
   const int s = item.x;
+  const int half = item.z;  // 0: the whole tile; 1 / 2: first / second half of its steps
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int kb0 = item.y * kPairKeys;
-  if (kb0 >= g.n) return;
+  if (kb0 >= g.n) {  // the work list holds no such tile
+    if (tid == 0) nxt = fetch_unit();
+    return;
+  }
 
   const int ka = kb0 + slice * 32;  // first key of this wave's slice
   const bool wave_active = ka < g.n;
@@ -74,24 +88,28 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   const int w_qs_max = qstart_of(g.p, ka + 31);
   const int q_begin = qstart_of(g.p, kb0);
   const int nqt = g.nq > q_begin ? (g.nq - q_begin + kBwdBlockQT - 1) / kBwdBlockQT : 0;
-  const int n_iter = nqt * a.group;
+  const int n_all = nqt * a.group;
+  const int it_lo = half == 2 ? n_all / 2 : 0;
+  const int n_iter = (half == 1 ? n_all / 2 : n_all) - it_lo;
+  const int head0 = nqt > 0 ? it_lo / nqt : 0;  // first step: q head hk * G + head0, query tile tile0
+  const int tile0 = it_lo - head0 * nqt;
 
   const bf16_t* kseq = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
   const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
-  const Loader ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane), ldv(a.v_st, wave, lane);
 
   // Iteration it covers q head hk * G + it / nqt and query tile it % nqt.  The
   // tile copies walk that order with running addresses (adds only), which keeps
   // the scalar work between barrier and first MFMA short.
   const uint32_t q_st32 = (uint32_t)a.q_st, o_st32 = (uint32_t)a.do_st;
-  const bf16_t* q_head = a.q + ((int64_t)g.start + q_begin) * a.q_st + (int64_t)(hk * a.group) * a.q_sh;
-  const bf16_t* o_head = a.dout + ((int64_t)g.start + q_begin) * a.do_st + (int64_t)(hk * a.group) * a.do_sh;
+  const int qh0 = hk * a.group + head0;
+  const bf16_t* q_head = a.q + ((int64_t)g.start + q_begin) * a.q_st + (int64_t)qh0 * a.q_sh;
+  const bf16_t* o_head = a.dout + ((int64_t)g.start + q_begin) * a.do_st + (int64_t)qh0 * a.do_sh;
   // one 4-byte row per wave: wave 0 lse2, the others delta (same data to the same place)
-  const float* r_head = (wave == 0 ? a.lse2 : a.delta) + (int64_t)(hk * a.group) * a.T + g.start + q_begin;
-  const bf16_t* i_q = q_head;
-  const bf16_t* i_o = o_head;
-  const float* i_r = r_head;
-  int i_qt = 0, i_rows = g.nq - q_begin;
+  const float* r_head = (wave == 0 ? a.lse2 : a.delta) + (int64_t)qh0 * a.T + g.start + q_begin;
+  const bf16_t* i_q = q_head + (int64_t)tile0 * kBwdBlockQT * a.q_st;
+  const bf16_t* i_o = o_head + (int64_t)tile0 * kBwdBlockQT * a.do_st;
+  const float* i_r = r_head + tile0 * kBwdBlockQT;
+  int i_qt = tile0, i_rows = g.nq - q_begin - tile0 * kBwdBlockQT;
   auto issue_next = [&](bf16_t* tq, bf16_t* to, float* tl, float* td) {
     ldq.issue_at(i_q, rows_bytes32(i_rows, q_st32, D), tq);
     ldo.issue_at(i_o, rows_bytes32(i_rows, o_st32, D), to);
@@ -142,8 +160,6 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
     dkacc[dt] = f32x16{};
     dvacc[dt] = f32x16{};
   }
-  const float c2 = a.scale_log2;
-  const TileLanes<D> tl(lane);
   // B operand of dP: V rows of this slice
   const bf16_t* const sVs = sV + (slice >> 1) * L::kElems + tl.op_base + (slice & 1) * 32 * L::kRowElems;
 
@@ -201,7 +217,7 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
       }
     }
   };
-  int s_qt = 0;  // query tile of the next step (the head only matters to the copies)
+  int s_qt = tile0;  // query tile of the next step (the head only matters to the copies)
   auto step = [&](const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
     const int qr = q_begin + s_qt * kBwdBlockQT + 32 * qh;
     if (++s_qt == nqt) s_qt = 0;
@@ -226,6 +242,7 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   }
   // With n_iter == 0 the V / K loads are still in flight here.
   wait_vmem();
+  if (tid == 0) nxt = fetch_unit();
 
   // Pair reduction: the second wave of each pair hands its partials over
   // through LDS (lane-major, conflict-free), first dV, then dK.
@@ -249,6 +266,83 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   hand_over(dvacc);
   hand_over(dkacc);
 
+  if (half != 0) {
+    // Split tile: each half publishes its partial sums in its own slot; the
+    // later of the two (per kv head) adds the other's and stores dK / dV.
+    // fp32 addition commutes, so the result does not depend on which is later.
+    // Slot layout: dK then dV, each four 16 KiB key-slice blocks of float4
+    // (dt * 4 + rq) * 64 + lane holding acc[dt][4 rq .. 4 rq + 3].
+    //
+    // Visibility without cache flushes: the slot is written by device-scope
+    // (write-through) stores, each wave waits for them to complete before the
+    // barrier that precedes the arrival count, and the later half reads the
+    // other slot with device-scope loads issued after the count has returned.
+    // The loads go straight to LDS (the dead tile buffers), so all 128 KiB are
+    // in flight at once.  A device-scope release / acquire fence pair would
+    // instead write back and invalidate the whole L2 of the XCD, which costs the
+    // other workgroups their cached Q / dO tiles.
+    constexpr int kDevScope = 16;  // buffer cache policy: coherent at device scope
+    constexpr uint32_t kSliceBytes = DT * 4 * 64 * 16;
+    const int ph = item.w * a.Hkv + hk;
+    const float* const slot_mine = a.split_buf + ((size_t)ph * 2 + (half - 1)) * kSplitSlotFloats;
+    const float* const slot_other = a.split_buf + ((size_t)ph * 2 + (2 - half)) * kSplitSlotFloats;
+    if (qh == 0) {
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc(slot_mine, kSplitSlotFloats * 4);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const uint32_t off = slice * kSliceBytes + (uint32_t)(((dt * 4 + rq) * 64 + lane) * 16);
+          const f32x4 k4 = {dkacc[dt][4 * rq], dkacc[dt][4 * rq + 1], dkacc[dt][4 * rq + 2], dkacc[dt][4 * rq + 3]};
+          const f32x4 v4 = {dvacc[dt][4 * rq], dvacc[dt][4 * rq + 1], dvacc[dt][4 * rq + 2], dvacc[dt][4 * rq + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, k4), rs, off, 0, kDevScope);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v4), rs, off + 4 * kSliceBytes, 0,
+                                                 kDevScope);
+        }
+      __asm__ volatile("" ::: "memory");
+      wait_vmem();  // the slot stores are complete
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const int prev = __hip_atomic_fetch_add(&a.split_ctr[ph], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (prev == 1) __hip_atomic_store(&a.split_ctr[ph], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      later = prev;
+    }
+    __syncthreads();
+    if (later == 0) return;  // the other half stores the tile
+    // Wave w copies block w of the other slot (dK slices 0-3, then dV) into LDS.
+    auto blk = [&](int i) -> bf16_t* {
+      return i == 0 ? sQ0 : i == 1 ? sO0 : i == 2 ? sQ1 : i == 3 ? sO1 : i == 4 ? sQ2 : i == 5 ? sO2
+           : i == 6 ? sV : sV + L::kElems;
+    };
+    static_assert(L::kElems * 2 >= (int)kSliceBytes, "a key-slice block fits one tile buffer");
+    {
+      const __amdgpu_buffer_rsrc_t ro = make_rsrc(slot_other, kSplitSlotFloats * 4);
+      bf16_t* const dst = blk(wave);
+#pragma unroll
+      for (int j = 0; j < DT * 4; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ro, (__attribute__((address_space(3))) void*)(dst + j * 512), 16,
+                                                 wave * kSliceBytes + (uint32_t)((j * 64 + lane) * 16), 0, 0,
+                                                 kDevScope);
+    }
+    stage_barrier<0>();
+    if (qh != 0) return;
+    const float* const ok = (const float*)blk(slice);
+    const float* const ov = (const float*)blk(4 + slice);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const f32x4 k4 = *(const f32x4*)&ok[((dt * 4 + rq) * 64 + lane) * 4];
+        const f32x4 v4 = *(const f32x4*)&ov[((dt * 4 + rq) * 64 + lane) * 4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dkacc[dt][4 * rq + e] += k4[e];
+          dvacc[dt][4 * rq + e] += v4[e];
+        }
+      }
+  }
+
   if (qh != 0 || !wave_active) return;
   const int kpos = ka + l32;
   if (kpos >= g.n) return;
@@ -267,16 +361,44 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
       *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tk, bf16x4);
       *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
     }
+  };
+
+  // Persistent workgroups (one per CU): the first unit is the workgroup's own
+  // index, later ones come from the queue, so the heaviest-first order of the
+  // list holds across XCDs and no workgroup waits for a dispatch slot.
+  const int n_units = a.cap_k * a.Hkv;
+  int unit = blockIdx.x;
+  for (;;) {
+    const int rank = unit / a.Hkv;
+    const int4 item = a.plan_k[rank];
+    if (item.x < 0) break;  // list padding: the rest of the list is padding too
+    int nxt = n_units;
+    run_unit(item, unit - rank * a.Hkv, nxt);
+    if (tid == 0) unit_next = nxt;
+    __syncthreads();
+    unit = unit_next;
+    __syncthreads();  // unit_next is rewritten after the next unit
+    if (unit >= n_units) break;
+  }
+  // The last workgroup to leave resets the queue for the next launch.
+  if (tid == 0 && __hip_atomic_fetch_add(&a.queue[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      (int)gridDim.x - 1) {
+    __hip_atomic_store(&a.queue[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&a.queue[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 }  // namespace
 
 hipError_t launch_bwd_dkdv_pair_bf16(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   static_assert(kPairKeys == kPlanTile, "work-list tiles are the dK / dV key tiles");
-  if (numseqs <= 0 || a.plan_cap == 0) return hipSuccess;
-  a.plan = a.plan_k;  // written by the DELTA stage's prologue
-  // workgroup r * Hkv + h: list entry r, kv head h
-  hipLaunchKernelGGL(dkdv_pair_kernel, dim3((unsigned)a.plan_cap * (unsigned)a.Hkv), dim3(kPairWaves * 64), 0,
+  static_assert(kPairKeys * kPairD * 2 == kSplitSlotFloats, "split slot = dK + dV of one key tile");
+  if (numseqs <= 0 || a.cap_k == 0) return hipSuccess;
+  // unit r * Hkv + h: list entry r (written by the DELTA stage's prologue), kv head h;
+  // one persistent workgroup per CU
+  const int64_t units = (int64_t)a.cap_k * a.Hkv;
+  const int grid = (int)(units < device_cu_count() ? units : device_cu_count());
+  hipLaunchKernelGGL(dkdv_pair_kernel, dim3((unsigned)grid), dim3(kPairWaves * 64), 0,
                      stream, a);
   return hipGetLastError();
 }

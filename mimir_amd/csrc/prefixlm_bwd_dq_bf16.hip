@@ -15,7 +15,7 @@ constexpr int kBlockK = 64;   // keys per LDS tile
 // so lse and delta are lane-local and dS^T feeds the B operand of dQ^T += K^T dS^T
 // directly; K^T fragments come from the row-major K tile via ds_read_b64_tr_b16.
 // Workgroup r * Hq + h takes head h of entry r of the query-tile work list
-// (prefixlm_plan.hip): longest key ranges first.
+// (prefixlm_prologue.hip): longest key ranges first.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
@@ -179,10 +179,9 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
 template <int D>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   static_assert(kBlockQ == kPlanTile, "work-list tiles are the dQ query tiles");
-  if (numseqs <= 0 || a.plan_cap == 0) return hipSuccess;
-  a.plan = a.plan_q;  // written by the DELTA stage's prologue
+  if (numseqs <= 0 || a.cap_q == 0) return hipSuccess;
   // workgroup r * Hq + h: list entry r, head h
-  hipLaunchKernelGGL(dq_kernel<D>, dim3((unsigned)a.plan_cap * (unsigned)a.Hq), dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(dq_kernel<D>, dim3((unsigned)a.cap_q * (unsigned)a.Hq), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

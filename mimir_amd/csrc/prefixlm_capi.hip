@@ -104,9 +104,9 @@ size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs,
 size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads, int32_t numseqs,
                                           int32_t max_seqlen_all) {
   if (total_tokens <= 0 || num_q_heads <= 0) return 0;
-  // float32 delta [Hq, T], float32 lse * log2(e) [Hq, T], then the dQ and dK/dV tile lists
-  return 2 * (size_t)total_tokens * (size_t)num_q_heads * sizeof(float) +
-         2 * (size_t)mimir::plan_capacity(total_tokens, numseqs, max_seqlen_all) * sizeof(int2);
+  // float32 delta [Hq, T], float32 lse * log2(e) [Hq, T], the dQ and dK/dV tile
+  // lists, the split counters and the split dK/dV partial slots
+  return mimir::bwd_workspace_layout(total_tokens, num_q_heads, numseqs, max_seqlen_all).total;
 }
 
 int mimir_prefixlm_check_metadata(const int32_t* prefix_lens, const int32_t* causal_lens,

@@ -272,10 +272,17 @@ namespace mimir {
 // The per-call work in front of the tile loops (prefixlm_prologue.hip), run as
 // one launch: tile work lists, the backward's delta rows, padding-row fills.
 //
-// Tile work lists: kind 0 holds 128-row query tiles (forward, dQ), kind 1
-// 128-key tiles (dK / dV).  A list of capacity plan_capacity() int2
-// (sequence, tile) entries is sorted by cost, descending, and padded with
-// (-1, -1); workgroup r * H + h of a consumer takes entry r for head h.
+// Tile work lists: kind 0 holds 128-row query tiles (forward, dQ) as int2
+// (sequence, tile); kind 1 holds 128-key tiles (dK / dV) as int4 (sequence,
+// tile, part, pair).  A list is sorted by cost, descending, and padded with
+// sequence -1; workgroup r * H + h of a consumer takes entry r for head h.
+//
+// Kind-1 items may be split: part 0 is a whole key tile; parts 1 and 2 are its
+// first and second half of the (q head, 64-query tile) steps, each adding into
+// dK / dV of the same keys.  Both halves write fp32 partials to the split slots
+// of pair `pair` and the later of the two (per kv head) adds them and stores
+// dK / dV (see SplitSlots).  Splitting evens out the workgroups when a few
+// heavy key tiles (the prefix tiles, which every query attends) dominate.
 constexpr int kPlanTile = 128;
 int plan_capacity(int total_tokens, int numseqs, int max_seqlen_all);
 
@@ -283,8 +290,28 @@ struct PlanArgs {
   const int32_t* cu_seqlens;
   const int32_t* prefix_lens;
   int numseqs, total_seqlen, is_causal, T, kind, group, cap;
-  int2* items;
+  void* items;     // int2 [cap] (kind 0) or int4 [cap] (kind 1)
+  // kind 1: split items costing more than (total cost * split_heads / slots) / 3,
+  // heaviest first and whole cost buckets at a time, up to max_pairs items;
+  // split_heads = 0 disables splitting.
+  int split_heads, max_pairs, slots;
+  int* zero;  // n_zero int32 set to 0 (the consumer's counters)
+  int n_zero;
 };
+
+// Split partials of the dK / dV kernel: per (pair, kv head) one arrival counter
+// and two slots (one per part) of fp32 dK then dV, 128 keys x 128 columns each.
+// Two more counters after them drive its work queue (next unit, finished
+// workgroups).
+constexpr int kSplitPairHeads = 384;              // most (pair, kv head) combinations per call
+constexpr int kSplitSlotFloats = 2 * 128 * 128;   // dK + dV partial of one part
+
+// Backward workspace sections (byte offsets, 256-byte aligned).
+struct BwdWorkspace {
+  size_t delta, lse2, plan_q, plan_k, counters, slots, total;
+  int cap_q, cap_k, pair_heads;
+};
+BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all);
 
 // delta[h, t] = sum_d O[t, h, d] * dO[t, h, d] and lse2[h, t] = lse[h, t] * log2(e), bf16 O / dO.
 struct DeltaArgs {
@@ -318,7 +345,9 @@ struct Prologue {
 };
 
 PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int numseqs, int total_seqlen,
-                   int is_causal, int total_tokens, int kind, int group, int cap, int2* items);
+                   int is_causal, int total_tokens, int kind, int group, int cap, void* items);
+// Compute units of the current device (cached per device).
+int device_cu_count();
 FillArgs fill_args(void* x, int64_t st, int64_t sh, float* lse, int64_t lse_sh, const int32_t* cu, int numseqs,
                    int total_seqlen, int T, int H, int D, int elem_bytes);
 hipError_t launch_prologue(const Prologue& pro, hipStream_t stream);

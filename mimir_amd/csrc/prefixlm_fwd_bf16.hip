@@ -2,7 +2,7 @@
 //
 // One workgroup = 4 waves = 128 query rows of one (sequence, query head); each
 // wave owns 32 rows.  Workgroup r * Hq + h takes head h of entry r of the tile
-// work list (prefixlm_plan.hip): query tiles sorted by key range, longest first.
+// work list (prefixlm_prologue.hip): query tiles sorted by key range, longest first.
 //
 // The kernel computes S^T = K Q^T on v_mfma_f32_32x32x16_bf16 so that every lane
 // holds one query column of the score tile: the softmax max/sum over keys is a
@@ -44,7 +44,7 @@ struct FwdArgs {
   int group;         // Hq / Hkv
   int total_seqlen;
   int is_causal;
-  const int2* plan;  // (sequence, query tile) per workgroup row, heaviest first (prefixlm_plan.hip)
+  const int2* plan;  // (sequence, query tile) per workgroup row, heaviest first (prefixlm_prologue.hip)
   float scale;       // softmax scale
   float scale_log2;  // softmax scale * log2(e)
 };

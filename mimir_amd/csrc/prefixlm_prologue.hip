@@ -73,31 +73,46 @@ __device__ int block_exclusive_scan(int v, int* wave_sums, int& total) {
   return before + x - v;
 }
 
+// Cost of tile t in 64-row steps of the consumer's loop (for kind 1 exactly
+// its iteration count G * query tiles).
 __device__ __forceinline__ int item_cost(int p, int nq, int kind, int group, int t) {
-  int c;
   if (kind == 0) {
     const int kend = max(p, min(t * kPlanTile + kPlanTile, nq));
-    c = (kend + 63) / 64;
-  } else {
-    const int q0 = qstart_of(p, t * kPlanTile);
-    c = nq > q0 ? group * ((nq - q0 + 63) / 64) : 0;
+    return (kend + 63) / 64;
   }
-  return min(c, kPlanBuckets - 1);
+  const int q0 = qstart_of(p, t * kPlanTile);
+  return nq > q0 ? group * ((nq - q0 + 63) / 64) : 0;
 }
+
+__device__ __forceinline__ int bucket_of(int cost) { return min(cost, kPlanBuckets - 1); }
 
 struct PlanSmem {
   int hist[kPlanBuckets];
   int first_item[kThreads];  // per sequence of the current chunk
   int p[kThreads], nq[kThreads];
   int wave_sums[kWaves];
+  double wave_dsums[kWaves];
+  int cut, pairs;
 };
+
+__device__ __forceinline__ void put_item(const PlanArgs& a, int pos, int s, int t, int part, int pair) {
+  if (pos >= a.cap) return;
+  if (a.kind == 0)
+    ((int2*)a.items)[pos] = make_int2(s, t);
+  else
+    ((int4*)a.items)[pos] = make_int4(s, t, part, pair);
+}
 
 // Visits every (sequence, tile) item, 256 sequences at a time: a scan of the
 // tile counts gives each sequence its first item, then the items are dealt to
 // the threads one each, so a single long sequence is spread over the workgroup
-// too.  Pass 1 counts items per cost bucket, pass 2 (kScatter) writes them.
+// too.  Items costing `cut` or more count as two halves.  Without kScatter the
+// visit adds each item (or half) to its cost bucket; with kScatter it takes the
+// next position of that bucket and writes the entry.  Returns this thread's
+// share of the total cost.
 template <bool kScatter>
-__device__ void walk_items(const PlanArgs& a, PlanSmem& sm) {
+__device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut) {
+  double cost_sum = 0.0;
   for (int base = 0; base < a.numseqs; base += kThreads) {
     const int s = base + (int)threadIdx.x;
     int nt = 0, p = 0, nq = 0;
@@ -121,39 +136,91 @@ __device__ void walk_items(const PlanArgs& a, PlanSmem& sm) {
         if (sm.first_item[j + step] <= i) j += step;
       const int t = i - sm.first_item[j];
       const int c = item_cost(sm.p[j], sm.nq[j], a.kind, a.group, t);
-      if constexpr (kScatter) {
-        const int pos = atomicAdd(&sm.hist[c], 1);
-        if (pos < a.cap) a.items[pos] = make_int2(base + j, t);
+      cost_sum += (double)c;
+      if (c >= cut) {
+        const int c1 = c / 2, c2 = c - c1;
+        if constexpr (kScatter) {
+          const int pair = atomicAdd(&sm.pairs, 1);
+          put_item(a, atomicAdd(&sm.hist[bucket_of(c1)], 1), base + j, t, 1, pair);
+          put_item(a, atomicAdd(&sm.hist[bucket_of(c2)], 1), base + j, t, 2, pair);
+        } else {
+          atomicAdd(&sm.hist[bucket_of(c1)], 1);
+          atomicAdd(&sm.hist[bucket_of(c2)], 1);
+        }
+      } else if constexpr (kScatter) {
+        put_item(a, atomicAdd(&sm.hist[bucket_of(c)], 1), base + j, t, 0, -1);
       } else {
-        atomicAdd(&sm.hist[c], 1);
+        atomicAdd(&sm.hist[bucket_of(c)], 1);
       }
     }
     __syncthreads();  // the chunk arrays are rewritten by the next chunk
   }
+  return cost_sum;
+}
+
+// Turns the bucket counts into start positions in descending cost order
+// (bucket c starts after all items of cost > c) and returns the item count.
+// Thread i owns buckets kPlanBuckets-1-16i down to kPlanBuckets-16-16i.  With
+// `max_pairs` > 0 it also finds the split cut: the smallest bucket above
+// `threshold` whose items and all heavier ones number at most max_pairs.
+__device__ int bucket_starts(PlanSmem& sm, double threshold, int max_pairs) {
+  int cnt[kBucketsPerThread];
+  int local = 0;
+#pragma unroll
+  for (int j = 0; j < kBucketsPerThread; ++j) {
+    cnt[j] = sm.hist[kPlanBuckets - 1 - (kBucketsPerThread * threadIdx.x + j)];
+    local += cnt[j];
+  }
+  int total;
+  int run = block_exclusive_scan(local, sm.wave_sums, total);
+  int cut = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < kBucketsPerThread; ++j) {
+    const int b = kPlanBuckets - 1 - (kBucketsPerThread * threadIdx.x + j);
+    sm.hist[b] = run;  // becomes the next free position of bucket b
+    run += cnt[j];     // items of cost >= b
+    if (max_pairs > 0 && (double)b > threshold && run <= max_pairs) cut = b;
+  }
+  if (max_pairs > 0 && cut != 0x7fffffff) atomicMin(&sm.cut, cut);
+  __syncthreads();
+  return total;
+}
+
+__device__ double block_sum(double v, PlanSmem& sm) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) sm.wave_dsums[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double total = 0.0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) total += sm.wave_dsums[i];
+  return total;
 }
 
 __device__ void plan_block(const PlanArgs& a) {
   __shared__ PlanSmem sm;
+  const bool split = a.kind == 1 && a.split_heads > 0 && a.max_pairs > 0 && a.slots > 0;
   for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
-  __syncthreads();
-  walk_items<false>(a, sm);
-  // Bucket starts in descending cost order: bucket c starts after all items of
-  // cost > c.  Thread i owns buckets kPlanBuckets-1-16i down to kPlanBuckets-16-16i.
-  int local = 0;
-#pragma unroll
-  for (int j = 0; j < kBucketsPerThread; ++j) local += sm.hist[kPlanBuckets - 1 - (kBucketsPerThread * threadIdx.x + j)];
-  int total;
-  int run = block_exclusive_scan(local, sm.wave_sums, total);
-#pragma unroll
-  for (int j = 0; j < kBucketsPerThread; ++j) {
-    const int b = kPlanBuckets - 1 - (kBucketsPerThread * threadIdx.x + j);
-    const int h = sm.hist[b];
-    sm.hist[b] = run;  // becomes the next free position of bucket b
-    run += h;
+  if (threadIdx.x == 0) {
+    sm.cut = 0x7fffffff;
+    sm.pairs = 0;
   }
+  for (int i = threadIdx.x; i < a.n_zero; i += kThreads) a.zero[i] = 0;
   __syncthreads();
-  walk_items<true>(a, sm);
-  for (int i = total + threadIdx.x; i < a.cap; i += kThreads) a.items[i] = make_int2(-1, -1);
+  const double mine = walk_items<false>(a, sm, 0x7fffffff);
+  double threshold = 0.0;
+  if (split)  // a third of the average per compute unit
+    threshold = block_sum(mine, sm) * a.split_heads / a.slots / 3.0;
+  int total = bucket_starts(sm, threshold, split ? a.max_pairs : 0);
+  const int cut = sm.cut;
+  if (cut != 0x7fffffff) {  // recount with the heavy items halved
+    for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
+    __syncthreads();
+    walk_items<false>(a, sm, cut);
+    total = bucket_starts(sm, 0.0, 0);
+  }
+  walk_items<true>(a, sm, cut);
+  for (int i = total + threadIdx.x; i < a.cap; i += kThreads) put_item(a, i, -1, -1, 0, -1);
 }
 
 // delta = rowsum(O * dO) and lse * log2(e) for 256 / (D / 8) (token, head) rows;
@@ -233,7 +300,7 @@ int plan_capacity(int total_tokens, int numseqs, int max_seqlen_all) {
 }
 
 PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int numseqs, int total_seqlen,
-                   int is_causal, int total_tokens, int kind, int group, int cap, int2* items) {
+                   int is_causal, int total_tokens, int kind, int group, int cap, void* items) {
   PlanArgs a;
   a.cu_seqlens = cu_seqlens;
   a.prefix_lens = prefix_lens;
@@ -245,7 +312,41 @@ PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int nu
   a.group = group;
   a.cap = cap;
   a.items = items;
+  a.split_heads = 0;
+  a.max_pairs = 0;
+  a.slots = 0;
+  a.zero = nullptr;
+  a.n_zero = 0;
   return a;
+}
+
+BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all) {
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  BwdWorkspace w;
+  const size_t rows = (size_t)(total_tokens > 0 ? total_tokens : 0) * (size_t)(num_q_heads > 0 ? num_q_heads : 0);
+  w.cap_q = plan_capacity(total_tokens, numseqs, max_seqlen_all);
+  const int64_t ph = (int64_t)w.cap_q * (num_q_heads > 0 ? num_q_heads : 0);
+  w.pair_heads = (int)(ph < kSplitPairHeads ? ph : kSplitPairHeads);
+  w.cap_k = w.cap_q + w.pair_heads;
+  w.delta = 0;
+  w.lse2 = align(w.delta + rows * sizeof(float));
+  w.plan_q = align(w.lse2 + rows * sizeof(float));
+  w.plan_k = align(w.plan_q + (size_t)w.cap_q * sizeof(int2));
+  w.counters = align(w.plan_k + (size_t)w.cap_k * sizeof(int4));
+  w.slots = align(w.counters + ((size_t)w.pair_heads + 2) * sizeof(int));
+  w.total = w.slots + (size_t)w.pair_heads * 2 * kSplitSlotFloats * sizeof(float);
+  return w;
+}
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev < 64) cached[dev] = n;
+  return n;
 }
 
 FillArgs fill_args(void* x, int64_t st, int64_t sh, float* lse, int64_t lse_sh, const int32_t* cu, int numseqs,

@@ -54,8 +54,26 @@ def test_workspace_bytes(lib):
     assert lib.mimir_prefixlm_fwd_workspace_bytes(16384, 8, 2048) == 8 * 16 * 8
     assert lib.mimir_prefixlm_fwd_workspace_bytes(16384, 1000, 4096) == (128 + 1000) * 8
     assert lib.mimir_prefixlm_fwd_workspace_bytes(0, 8, 2048) == 0
-    assert lib.mimir_prefixlm_bwd_workspace_bytes(16384, 16, 8, 2048) == 2 * 16384 * 16 * 4 + 2 * 8 * 16 * 8
+    for args in ((16384, 16, 8, 2048), (2048, 8, 4, 512), (16384, 16, 1000, 4096), (100, 3, 1, 100)):
+        assert lib.mimir_prefixlm_bwd_workspace_bytes(*args) == _bwd_workspace(*args), args
     assert lib.mimir_prefixlm_bwd_workspace_bytes(0, 16, 8, 2048) == 0
+
+
+def _bwd_workspace(T, hq, numseqs, max_len):
+    """Backward workspace: 256-byte aligned sections delta and lse*log2(e) (float32 [Hq, T]), the
+    query-tile list (int2 per tile), the key-tile list (int4 per tile plus one per possible split pair),
+    one int32 counter per split (pair, kv head) plus two work-queue counters, and two float32 slots of
+    2 * 128 * 128 per split (pair, kv head)."""
+    def align(x):
+        return (x + 255) // 256 * 256
+    cap = min(numseqs * -(-max_len // 128), -(-T // 128) + numseqs)
+    pair_heads = min(384, cap * hq)
+    lse2 = align(T * hq * 4)
+    plan_q = align(lse2 + T * hq * 4)
+    plan_k = align(plan_q + cap * 8)
+    counters = align(plan_k + (cap + pair_heads) * 16)
+    slots = align(counters + (pair_heads + 2) * 4)
+    return slots + pair_heads * 2 * 2 * 128 * 128 * 4
 
 
 def _c_layout(struct_name, fields):
