@@ -244,27 +244,46 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   wait_vmem();
   if (tid == 0) nxt = fetch_unit();
 
-  // Pair reduction: the second wave of each pair hands its partials over
-  // through LDS (lane-major, conflict-free), first dV, then dK.
-  float* const part = (float*)(slice == 0 ? sQ0 : slice == 1 ? sO0 : slice == 2 ? sQ1 : sO1) + lane;
-  auto hand_over = [&](f32x16 (&acc)[DT]) {
-    __syncthreads();  // every wave is done with the stage buffers / the previous round
+  // The tile buffers are free after the loop: eight 16 KiB blocks for the
+  // reductions and the store transposition below.
+  auto blk = [&](int i) -> bf16_t* {
+    return i == 0 ? sQ0 : i == 1 ? sO0 : i == 2 ? sQ1 : i == 3 ? sO1 : i == 4 ? sQ2 : i == 5 ? sO2
+         : i == 6 ? sV : sV + L::kElems;
+  };
+  static_assert(L::kElems * 2 >= DT * 4 * 64 * 16, "a key slice's dK or dV (fp32) fits one block");
+
+  // Pair reduction: the second wave of each pair hands its dK and dV partials
+  // over through LDS in one round (float4 per lane, lane-major: conflict-free).
+  __syncthreads();  // every wave is done with the stage buffers
+  {
+    f32x4* const pk = (f32x4*)blk(slice) + lane;
+    f32x4* const pv = (f32x4*)blk(4 + slice) + lane;
     if (qh == 1) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) part[(16 * dt + r) * 64] = acc[dt][r];
+        for (int rq = 0; rq < 4; ++rq) {
+          pk[(dt * 4 + rq) * 64] = f32x4{dkacc[dt][4 * rq], dkacc[dt][4 * rq + 1], dkacc[dt][4 * rq + 2],
+                                         dkacc[dt][4 * rq + 3]};
+          pv[(dt * 4 + rq) * 64] = f32x4{dvacc[dt][4 * rq], dvacc[dt][4 * rq + 1], dvacc[dt][4 * rq + 2],
+                                         dvacc[dt][4 * rq + 3]};
+        }
     }
     __syncthreads();
     if (qh == 0) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[dt][r] += part[(16 * dt + r) * 64];
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 k4 = pk[(dt * 4 + rq) * 64], v4 = pv[(dt * 4 + rq) * 64];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dkacc[dt][4 * rq + e] += k4[e];
+            dvacc[dt][4 * rq + e] += v4[e];
+          }
+        }
     }
-  };
-  hand_over(dvacc);
-  hand_over(dkacc);
+  }
 
   if (half != 0) {
     // Split tile: each half publishes its partial sums in its own slot; the
@@ -311,11 +330,6 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
     __syncthreads();
     if (later == 0) return;  // the other half stores the tile
     // Wave w copies block w of the other slot (dK slices 0-3, then dV) into LDS.
-    auto blk = [&](int i) -> bf16_t* {
-      return i == 0 ? sQ0 : i == 1 ? sO0 : i == 2 ? sQ1 : i == 3 ? sO1 : i == 4 ? sQ2 : i == 5 ? sO2
-           : i == 6 ? sV : sV + L::kElems;
-    };
-    static_assert(L::kElems * 2 >= (int)kSliceBytes, "a key-slice block fits one tile buffer");
     {
       const __amdgpu_buffer_rsrc_t ro = make_rsrc(slot_other, kSplitSlotFloats * 4);
       bf16_t* const dst = blk(wave);
@@ -326,41 +340,67 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
                                                  kDevScope);
     }
     stage_barrier<0>();
-    if (qh != 0) return;
-    const float* const ok = (const float*)blk(slice);
-    const float* const ov = (const float*)blk(4 + slice);
+    if (qh == 0) {
+      const f32x4* const ok = (const f32x4*)blk(slice) + lane;
+      const f32x4* const ov = (const f32x4*)blk(4 + slice) + lane;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 k4 = ok[(dt * 4 + rq) * 64], v4 = ov[(dt * 4 + rq) * 64];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dkacc[dt][4 * rq + e] += k4[e];
+            dvacc[dt][4 * rq + e] += v4[e];
+          }
+        }
+    }
+  }
+
+  // dK (scaled) and dV to bf16, transposed through LDS so that every global
+  // store writes whole 256-byte key rows: rows 0-63 / 64-127 of dK in blocks
+  // 0 / 1, of dV in blocks 2 / 3, 16-byte chunks XOR-swizzled by row.
+  __syncthreads();  // the reduction reads of blocks 0-7 are done
+  // The lane index is re-materialized here (opaque to the optimizer), so that
+  // the store offsets below are computed now instead of being hoisted to the
+  // kernel entry and spilled across the tile loop.
+  int elane = lane;
+  __asm__ volatile("" : "+v"(elane));
+  if (qh == 0) {
+    char* const tk = (char*)blk(slice >> 1);
+    char* const tv = (char*)blk(2 + (slice >> 1));
+    const int rb = (slice & 1) * 32 + (elane & 31);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const f32x4 k4 = *(const f32x4*)&ok[((dt * 4 + rq) * 64 + lane) * 4];
-        const f32x4 v4 = *(const f32x4*)&ov[((dt * 4 + rq) * 64 + lane) * 4];
+      for (int rg = 0; rg < 4; ++rg) {
+        f32x4 t4k, t4v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          dkacc[dt][4 * rq + e] += k4[e];
-          dvacc[dt][4 * rq + e] += v4[e];
+          t4k[e] = dkacc[dt][4 * rg + e] * a.scale;
+          t4v[e] = dvacc[dt][4 * rg + e];
         }
+        const int off = rb * 256 + (((4 * dt + rg) ^ (rb & 15)) * 16) + 8 * (elane >> 5);
+        *(bf16x4*)(tk + off) = __builtin_convertvector(t4k, bf16x4);
+        *(bf16x4*)(tv + off) = __builtin_convertvector(t4v, bf16x4);
       }
   }
-
-  if (qh != 0 || !wave_active) return;
-  const int kpos = ka + l32;
-  if (kpos >= g.n) return;
-  bf16_t* krow = a.dk + (int64_t)(g.start + kpos) * a.dk_st + (int64_t)hk * a.dk_sh;
-  bf16_t* vrow = a.dv + (int64_t)(g.start + kpos) * a.dv_st + (int64_t)hk * a.dv_sh;
+  __syncthreads();
+  static_assert(D * 2 == 16 * 16, "a key row is 16 chunks of 16 bytes");
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      f32x4 tk, tv;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        tk[e] = dkacc[dt][4 * rg + e] * a.scale;
-        tv[e] = dvacc[dt][4 * rg + e];
-      }
-      *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tk, bf16x4);
-      *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
+  for (int i = 0; i < 4; ++i) {
+    const int row = (i * kPairWaves + wave) * 4 + (elane >> 4);  // 0 .. 127
+    const int chunk = elane & 15;
+    const int rb = row & 63;
+    const int off = rb * 256 + ((chunk ^ (rb & 15)) * 16);
+    const i32x4 k16 = *(const i32x4*)((const char*)blk(row >> 6) + off);
+    const i32x4 v16 = *(const i32x4*)((const char*)blk(2 + (row >> 6)) + off);
+    const int key = kb0 + row;
+    if (key < g.n) {
+      *(i32x4*)(a.dk + (int64_t)(g.start + key) * a.dk_st + (int64_t)hk * a.dk_sh + chunk * 8) = k16;
+      *(i32x4*)(a.dv + (int64_t)(g.start + key) * a.dv_st + (int64_t)hk * a.dv_sh + chunk * 8) = v16;
     }
+  }
   };
 
   // Persistent workgroups (one per CU): the first unit is the workgroup's own

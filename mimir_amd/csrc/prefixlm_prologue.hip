@@ -223,29 +223,45 @@ __device__ void plan_block(const PlanArgs& a) {
   for (int i = total + threadIdx.x; i < a.cap; i += kThreads) put_item(a, i, -1, -1, 0, -1);
 }
 
-// delta = rowsum(O * dO) and lse * log2(e) for 256 / (D / 8) (token, head) rows;
-// the tile loops then form P = exp2(S * scale * log2(e) - lse2) with one FMA.
+// delta = rowsum(O * dO) and lse * log2(e) for kDeltaPasses * 256 / (D / 8)
+// (token, head) rows, D / 8 lanes per row; every pass's loads are issued before
+// the first reduction.  The tile loops then form P = exp2(S * scale * log2(e) -
+// lse2) with one FMA.
+constexpr int kDeltaPasses = 4;
+
 template <int D>
 __device__ void delta_block(const DeltaArgs& a, int b) {
-  constexpr int LPR = D / 8;  // lanes per row
-  const int64_t gid = (int64_t)b * kThreads + threadIdx.x;
-  const int64_t row = gid / LPR;  // row = t * Hq + h
-  const int c = (int)(gid % LPR);
-  const bool valid = row < (int64_t)a.T * a.Hq;
-  const int t = valid ? (int)(row / a.Hq) : 0;
-  const int h = valid ? (int)(row % a.Hq) : 0;
-  float acc = 0.f;
-  if (valid) {
-    const bf16x8 ov = *(const bf16x8*)&a.o[(int64_t)t * a.o_st + (int64_t)h * a.o_sh + c * 8];
-    const bf16x8 dv = *(const bf16x8*)&a.dout[(int64_t)t * a.do_st + (int64_t)h * a.do_sh + c * 8];
+  constexpr int LPR = D / 8;            // lanes per row
+  constexpr int RPP = kThreads / LPR;   // rows per pass
+  const int c = threadIdx.x % LPR;
+  const int64_t rows = (int64_t)a.T * a.Hq;
+  bf16x8 ov[kDeltaPasses], dv[kDeltaPasses];
+  int t[kDeltaPasses], h[kDeltaPasses];
+  bool valid[kDeltaPasses];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (float)ov[e] * (float)dv[e];
+  for (int i = 0; i < kDeltaPasses; ++i) {
+    const int64_t row = ((int64_t)b * kDeltaPasses + i) * RPP + threadIdx.x / LPR;  // row = t * Hq + h
+    valid[i] = row < rows;
+    t[i] = valid[i] ? (int)(row / a.Hq) : 0;
+    h[i] = valid[i] ? (int)(row - (int64_t)t[i] * a.Hq) : 0;
+    if (valid[i]) {
+      ov[i] = *(const bf16x8*)&a.o[(int64_t)t[i] * a.o_st + (int64_t)h[i] * a.o_sh + c * 8];
+      dv[i] = *(const bf16x8*)&a.dout[(int64_t)t[i] * a.do_st + (int64_t)h[i] * a.do_sh + c * 8];
+    }
   }
 #pragma unroll
-  for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (valid && c == 0) {
-    a.delta[(int64_t)h * a.T + t] = acc;
-    a.lse2[(int64_t)h * a.T + t] = a.lse[(int64_t)h * a.lse_sh + t] * kLog2e;
+  for (int i = 0; i < kDeltaPasses; ++i) {
+    float acc = 0.f;
+    if (valid[i]) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)ov[i][e] * (float)dv[i][e];
+    }
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (valid[i] && c == 0) {
+      a.delta[(int64_t)h[i] * a.T + t[i]] = acc;
+      a.lse2[(int64_t)h[i] * a.T + t[i]] = a.lse[(int64_t)h[i] * a.lse_sh + t[i]] * kLog2e;
+    }
   }
 }
 
@@ -369,7 +385,8 @@ hipError_t launch_prologue(const Prologue& pro, hipStream_t stream) {
   if (pro.has_delta && (int64_t)pro.delta.T * pro.delta.Hq > 0) {
     delta_d = pro.delta.D;
     const int64_t threads = (int64_t)pro.delta.T * pro.delta.Hq * (delta_d / 8);
-    a.delta_blocks = (int)((threads + kThreads - 1) / kThreads);
+    const int64_t per_block = (int64_t)kThreads * kDeltaPasses;
+    a.delta_blocks = (int)((threads + per_block - 1) / per_block);
   }
   a.nfill = 0;
   a.fill_blocks = 0;
