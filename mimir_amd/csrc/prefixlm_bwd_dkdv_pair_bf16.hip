@@ -357,50 +357,24 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
     }
   }
 
-  // dK (scaled) and dV to bf16, transposed through LDS so that every global
-  // store writes whole 256-byte key rows: rows 0-63 / 64-127 of dK in blocks
-  // 0 / 1, of dV in blocks 2 / 3, 16-byte chunks XOR-swizzled by row.
-  __syncthreads();  // the reduction reads of blocks 0-7 are done
-  // The lane index is re-materialized here (opaque to the optimizer), so that
-  // the store offsets below are computed now instead of being hoisted to the
-  // kernel entry and spilled across the tile loop.
-  int elane = lane;
-  __asm__ volatile("" : "+v"(elane));
-  if (qh == 0) {
-    char* const tk = (char*)blk(slice >> 1);
-    char* const tv = (char*)blk(2 + (slice >> 1));
-    const int rb = (slice & 1) * 32 + (elane & 31);
+  if (qh != 0 || !wave_active) return;
+  const int kpos = ka + l32;
+  if (kpos >= g.n) return;
+  bf16_t* krow = a.dk + (int64_t)(g.start + kpos) * a.dk_st + (int64_t)hk * a.dk_sh;
+  bf16_t* vrow = a.dv + (int64_t)(g.start + kpos) * a.dv_st + (int64_t)hk * a.dv_sh;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        f32x4 t4k, t4v;
+    for (int rg = 0; rg < 4; ++rg) {
+      f32x4 tk, tv;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          t4k[e] = dkacc[dt][4 * rg + e] * a.scale;
-          t4v[e] = dvacc[dt][4 * rg + e];
-        }
-        const int off = rb * 256 + (((4 * dt + rg) ^ (rb & 15)) * 16) + 8 * (elane >> 5);
-        *(bf16x4*)(tk + off) = __builtin_convertvector(t4k, bf16x4);
-        *(bf16x4*)(tv + off) = __builtin_convertvector(t4v, bf16x4);
+      for (int e = 0; e < 4; ++e) {
+        tk[e] = dkacc[dt][4 * rg + e] * a.scale;
+        tv[e] = dvacc[dt][4 * rg + e];
       }
-  }
-  __syncthreads();
-  static_assert(D * 2 == 16 * 16, "a key row is 16 chunks of 16 bytes");
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (i * kPairWaves + wave) * 4 + (elane >> 4);  // 0 .. 127
-    const int chunk = elane & 15;
-    const int rb = row & 63;
-    const int off = rb * 256 + ((chunk ^ (rb & 15)) * 16);
-    const i32x4 k16 = *(const i32x4*)((const char*)blk(row >> 6) + off);
-    const i32x4 v16 = *(const i32x4*)((const char*)blk(2 + (row >> 6)) + off);
-    const int key = kb0 + row;
-    if (key < g.n) {
-      *(i32x4*)(a.dk + (int64_t)(g.start + key) * a.dk_st + (int64_t)hk * a.dk_sh + chunk * 8) = k16;
-      *(i32x4*)(a.dv + (int64_t)(g.start + key) * a.dv_st + (int64_t)hk * a.dv_sh + chunk * 8) = v16;
+      *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tk, bf16x4);
+      *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
     }
-  }
   };
 
   // Persistent workgroups (one per CU): the first unit is the workgroup's own
