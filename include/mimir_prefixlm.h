@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MIMIR_PREFIXLM_ABI_VERSION 2
+#define MIMIR_PREFIXLM_ABI_VERSION 3
 
 /* Element types of q/k/v/out/dout/dq/dk/dv (lse and the workspace are float32). */
 enum MimirDType {
@@ -86,6 +86,16 @@ typedef struct MimirPrefixLMFwdParams {
   float softmax_scale;        /* > 0; the reference uses 1/sqrt(D) */
   void* workspace;            /* device memory, >= mimir_prefixlm_fwd_workspace_bytes(); 16-byte aligned */
   size_t workspace_bytes;
+  /* Optional sigmoid output gate (NULL: none).  With a gate the forward also
+   * writes gated_out = sigmoid(gate) * out, rounded as the reference's
+   * torch.sigmoid(gate) * attn_output in the element type
+   * (src/mimir/model/layers.py:239): s = round(sigmoid(gate)), then
+   * round(s * round(attention)).  out keeps the ungated attention output, which
+   * the backward needs. */
+  const void* gate;           /* [T, Hq, D] */
+  int64_t gate_stride_token, gate_stride_head;
+  void* gated_out;            /* [T, Hq, D]; required with a gate */
+  int64_t gated_out_stride_token, gated_out_stride_head;
 } MimirPrefixLMFwdParams;
 
 typedef struct MimirPrefixLMBwdParams {
@@ -120,8 +130,19 @@ typedef struct MimirPrefixLMBwdParams {
   int32_t is_causal;
   int32_t dtype;
   float softmax_scale;
-  void* workspace;            /* device memory, >= mimir_prefixlm_bwd_workspace_bytes() */
+  void* workspace;            /* device memory, >= mimir_prefixlm_bwd_workspace_size(params) */
   size_t workspace_bytes;
+  /* Optional sigmoid output gate (NULL: none), the backward of
+   * gated_out = sigmoid(gate) * out.  With a gate, `dout` is the gradient of
+   * gated_out and `out` the ungated attention output; the DELTA stage forms the
+   * attention's upstream gradient round(dout * s) in the workspace, delta from
+   * it, and dgate = round(round(dout * out) * (1 - s) * s) with s =
+   * round(sigmoid(gate)), in the order torch's autograd evaluates the reference
+   * expression (layers.py:239; sigmoid_backward = grad * (1 - y) * y). */
+  const void* gate;           /* [T, Hq, D] */
+  int64_t gate_stride_token, gate_stride_head;
+  void* dgate;                /* [T, Hq, D]; required with a gate */
+  int64_t dgate_stride_token, dgate_stride_head;
 } MimirPrefixLMBwdParams;
 
 /* Bytes of device workspace the forward needs: the heaviest-first tile work list
@@ -163,6 +184,40 @@ int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* params, int stages, 
  * read them, and DKDV leaves the counters at zero. */
 size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads, int32_t numseqs,
                                           int32_t max_seqlen_all);
+
+/* Bytes of backward workspace for these parameters: mimir_prefixlm_bwd_workspace_bytes
+ * plus, with a gate, the attention's upstream gradient [T, Hq, D] in the element type.
+ * Only the size fields, head_dim, dtype and gate are read. */
+size_t mimir_prefixlm_bwd_workspace_size(const MimirPrefixLMBwdParams* params);
+
+/* Rotary position embedding on [T, H, D] rows, rotate-half convention
+ * (reference: src/mimir/model/layers.py:24-40, apply_rotary_pos_emb on the q / k
+ * splits of the fused projection, layers.py:183-189), cos / sin float32 [T, D]:
+ *
+ *   inverse == 0:  y = round(x * cos + rotate_half(x) * sin)   (fp32 math, one rounding)
+ *   inverse != 0:  the gradient of that map, x_grad from y_grad, rounded as torch's
+ *                  autograd does for the reference expression: each of the two
+ *                  contributions (y_grad * cos and the rotate_half part of
+ *                  y_grad * sin) is rounded to the element type, then their sum.
+ *
+ * rotate_half(x) = cat(-x[D/2:], x[:D/2]).  y may alias x (same pointer and
+ * strides): every element pair is read before it is written.  bf16 needs
+ * D % 16 == 0, float32 D % 8 == 0; rows 16-byte aligned. */
+typedef struct MimirRopeParams {
+  const void* x;              /* [T, H, D] */
+  void* y;                    /* [T, H, D] */
+  const float* cos;           /* [T, D] float32 */
+  const float* sin;           /* [T, D] float32 */
+  int64_t x_stride_token, x_stride_head;
+  int64_t y_stride_token, y_stride_head;
+  int64_t cs_stride_token;    /* cos / sin row stride (elements) */
+  int32_t total_tokens;       /* T */
+  int32_t num_heads;          /* H */
+  int32_t head_dim;           /* D */
+  int32_t dtype;              /* enum MimirDType */
+  int32_t inverse;
+} MimirRopeParams;
+int mimir_prefixlm_rope(const MimirRopeParams* params, void* stream);
 
 /* Device-side metadata check: writes to *bad_seq (device int32) the first s in
  * [0, numseqs) with prefix_lens[s] + causal_lens[s] != cu_seqlens[s+1] - cu_seqlens[s]

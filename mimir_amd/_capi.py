@@ -16,7 +16,7 @@ from pathlib import Path
 
 # MIMIR_PREFIXLM_LIB overrides the in-tree library (e.g. to A/B two builds).
 LIB_PATH = Path(os.environ.get("MIMIR_PREFIXLM_LIB") or Path(__file__).resolve().parent / "_lib" / "libmimir_prefixlm.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_FLOAT32 = 0
 DTYPE_BFLOAT16 = 1
@@ -45,6 +45,8 @@ class FwdParams(ctypes.Structure):
         ("numseqs", _i32), ("total_seqlen", _i32), ("max_seqlen_all", _i32), ("is_causal", _i32),
         ("dtype", _i32), ("softmax_scale", ctypes.c_float),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("gate", _vp), ("gate_stride_token", _i64), ("gate_stride_head", _i64),
+        ("gated_out", _vp), ("gated_out_stride_token", _i64), ("gated_out_stride_head", _i64),
     ]
 
 
@@ -66,6 +68,18 @@ class BwdParams(ctypes.Structure):
         ("numseqs", _i32), ("total_seqlen", _i32), ("max_seqlen_all", _i32), ("is_causal", _i32),
         ("dtype", _i32), ("softmax_scale", ctypes.c_float),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("gate", _vp), ("gate_stride_token", _i64), ("gate_stride_head", _i64),
+        ("dgate", _vp), ("dgate_stride_token", _i64), ("dgate_stride_head", _i64),
+    ]
+
+
+class RopeParams(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("y", _vp), ("cos", _vp), ("sin", _vp),
+        ("x_stride_token", _i64), ("x_stride_head", _i64),
+        ("y_stride_token", _i64), ("y_stride_head", _i64),
+        ("cs_stride_token", _i64),
+        ("total_tokens", _i32), ("num_heads", _i32), ("head_dim", _i32), ("dtype", _i32), ("inverse", _i32),
     ]
 
 
@@ -81,6 +95,8 @@ EXPORTED_SYMBOLS = (
     "mimir_prefixlm_bwd_stages",
     "mimir_prefixlm_fwd_workspace_bytes",
     "mimir_prefixlm_bwd_workspace_bytes",
+    "mimir_prefixlm_bwd_workspace_size",
+    "mimir_prefixlm_rope",
     "mimir_prefixlm_check_metadata",
     "mimir_prefixlm_last_error",
     "mimir_prefixlm_abi_version",
@@ -118,6 +134,10 @@ def load() -> ctypes.CDLL:
         lib.mimir_prefixlm_fwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mimir_prefixlm_bwd_workspace_bytes.argtypes = [_i32, _i32, _i32, _i32]
         lib.mimir_prefixlm_bwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.mimir_prefixlm_bwd_workspace_size.argtypes = [ctypes.POINTER(BwdParams)]
+        lib.mimir_prefixlm_bwd_workspace_size.restype = ctypes.c_size_t
+        lib.mimir_prefixlm_rope.argtypes = [ctypes.POINTER(RopeParams), _vp]
+        lib.mimir_prefixlm_rope.restype = ctypes.c_int
         lib.mimir_prefixlm_check_metadata.argtypes = [_vp, _vp, _vp, _i32, _vp, _vp]
         lib.mimir_prefixlm_check_metadata.restype = ctypes.c_int
         lib.mimir_prefixlm_last_error.argtypes = []

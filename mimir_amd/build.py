@@ -46,6 +46,7 @@ SOURCES = [
     "prefixlm_bwd_dkdv_pair_bf16.hip",
     "prefixlm_f32.hip",
     "prefixlm_prologue.hip",
+    "prefixlm_layer.hip",
 ]
 
 

@@ -41,7 +41,9 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   a.dq = (bf16_t*)p.dq;
   a.dk = (bf16_t*)p.dk;
   a.dv = (bf16_t*)p.dv;
-  const BwdWorkspace ws = bwd_workspace_layout(p.total_tokens, p.num_q_heads, p.numseqs, p.max_seqlen_all);
+  const bool gated = p.gate != nullptr;
+  const BwdWorkspace ws = bwd_workspace_layout(p.total_tokens, p.num_q_heads, p.numseqs, p.max_seqlen_all,
+                                               gated ? (size_t)p.total_tokens * p.num_q_heads * D * 2 : 0);
   char* const wsb = (char*)p.workspace;
   a.delta = (float*)(wsb + ws.delta);
   a.lse2 = (float*)(wsb + ws.lse2);
@@ -60,6 +62,11 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   a.v_st = p.v_stride_token; a.v_sh = p.v_stride_head;
   a.o_st = p.out_stride_token; a.o_sh = p.out_stride_head;
   a.do_st = p.dout_stride_token; a.do_sh = p.dout_stride_head;
+  if (gated) {  // the tile kernels read the upstream gradient the DELTA stage forms in the workspace
+    a.dout = (const bf16_t*)(wsb + ws.dout);
+    a.do_st = (int64_t)p.num_q_heads * D;
+    a.do_sh = D;
+  }
   a.dq_st = p.dq_stride_token; a.dq_sh = p.dq_stride_head;
   a.dk_st = p.dk_stride_token; a.dk_sh = p.dk_stride_head;
   a.dv_st = p.dv_stride_token; a.dv_sh = p.dv_stride_head;
@@ -75,9 +82,16 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
 
   if (stages & MIMIR_BWD_STAGE_DELTA) {
     DeltaArgs& d = pro.delta;
-    d.o = a.o; d.dout = a.dout; d.lse = a.lse; d.delta = a.delta; d.lse2 = a.lse2;
-    d.o_st = a.o_st; d.o_sh = a.o_sh; d.do_st = a.do_st; d.do_sh = a.do_sh; d.lse_sh = a.lse_sh;
+    d.o = a.o; d.dout = (const bf16_t*)p.dout; d.lse = a.lse; d.delta = a.delta; d.lse2 = a.lse2;
+    d.o_st = a.o_st; d.o_sh = a.o_sh; d.do_st = p.dout_stride_token; d.do_sh = p.dout_stride_head;
+    d.lse_sh = a.lse_sh;
     d.T = a.T; d.Hq = a.Hq; d.D = D;
+    d.gate = gated ? (const bf16_t*)p.gate : nullptr;
+    d.dgate = (bf16_t*)p.dgate;
+    d.dout_s = (bf16_t*)a.dout;
+    d.g_st = p.gate_stride_token; d.g_sh = p.gate_stride_head;
+    d.dg_st = p.dgate_stride_token; d.dg_sh = p.dgate_stride_head;
+    d.ds_st = a.do_st; d.ds_sh = a.do_sh;
     pro.has_delta = 1;
     // both tile lists: the dK/dV stage reads kind 1, the dQ stage kind 0
     PlanArgs pk = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal, p.total_tokens,

@@ -101,6 +101,16 @@ size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs,
   return (size_t)mimir::plan_capacity(total_tokens, numseqs, max_seqlen_all) * sizeof(int2);
 }
 
+size_t mimir_prefixlm_bwd_workspace_size(const MimirPrefixLMBwdParams* p) {
+  if (p == nullptr || p->total_tokens <= 0 || p->num_q_heads <= 0) return 0;
+  const size_t dout_bytes = p->gate != nullptr ? (size_t)p->total_tokens * (size_t)p->num_q_heads *
+                                                     (size_t)(p->head_dim > 0 ? p->head_dim : 0) *
+                                                     (size_t)elem_bytes_of(p->dtype)
+                                               : 0;
+  return mimir::bwd_workspace_layout(p->total_tokens, p->num_q_heads, p->numseqs, p->max_seqlen_all, dout_bytes)
+      .total;
+}
+
 size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_heads, int32_t numseqs,
                                           int32_t max_seqlen_all) {
   if (total_tokens <= 0 || num_q_heads <= 0) return 0;
@@ -143,16 +153,28 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* p, void* stream_) {
   if (need > 0 && (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace)))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +
                                                 std::to_string(need) + " bytes");
+  if (p->gate != nullptr) {
+    if ((rc = check_operand("gate", p->gate, p->gate_stride_token, p->gate_stride_head, D, dt, rows))) return rc;
+    if ((rc = check_operand("gated_out", p->gated_out, p->gated_out_stride_token, p->gated_out_stride_head, D, dt,
+                            rows)))
+      return rc;
+  }
   mimir::Prologue pro;
   pro.fill[pro.nfill++] = mimir::fill_args(p->out, p->out_stride_token, p->out_stride_head, p->lse,
                                            p->lse_stride_head, p->cu_seqlens, p->numseqs, p->total_seqlen,
                                            p->total_tokens, p->num_q_heads, D, elem_bytes_of(dt));
   hipError_t e;
   if (dt == MIMIR_DTYPE_BFLOAT16) {
+    // gated_out rows outside the attended rows are sigmoid(gate) * 0 = 0
+    if (p->gate != nullptr)
+      pro.fill[pro.nfill++] = mimir::fill_args(p->gated_out, p->gated_out_stride_token, p->gated_out_stride_head,
+                                               nullptr, 0, p->cu_seqlens, p->numseqs, p->total_seqlen,
+                                               p->total_tokens, p->num_q_heads, D, elem_bytes_of(dt));
     e = mimir_launch_fwd_bf16(*p, pro, stream);
   } else {
     e = mimir::launch_prologue(pro, stream);
     if (e == hipSuccess) e = mimir_launch_fwd_f32(*p, stream);
+    if (e == hipSuccess && p->gate != nullptr) e = mimir::launch_gate_fwd_f32(*p, stream);
   }
   return hip_status(e, "forward launch");
 }
@@ -184,8 +206,12 @@ int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* p, int stages, void*
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "lse head stride is smaller than the packed length");
   if (p->numseqs > 0 && (p->prefix_lens == nullptr || p->cu_seqlens == nullptr))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "metadata pointer is NULL");
-  const size_t need =
-      mimir_prefixlm_bwd_workspace_bytes(p->total_tokens, p->num_q_heads, p->numseqs, p->max_seqlen_all);
+  if (p->gate != nullptr) {
+    if ((rc = check_operand("gate", p->gate, p->gate_stride_token, p->gate_stride_head, D, dt, rows))) return rc;
+    if ((rc = check_operand("dgate", p->dgate, p->dgate_stride_token, p->dgate_stride_head, D, dt, rows)))
+      return rc;
+  }
+  const size_t need = mimir_prefixlm_bwd_workspace_size(p);
   if (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +
                                                 std::to_string(need) + " bytes");
@@ -203,11 +229,53 @@ int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* p, int stages, void*
   hipError_t e;
   if (dt == MIMIR_DTYPE_BFLOAT16) {
     e = mimir_launch_bwd_bf16(*p, pro, stream, stages);
-  } else {
+  } else if (p->gate == nullptr) {
     e = mimir::launch_prologue(pro, stream);
     if (e == hipSuccess) e = mimir_launch_bwd_f32(*p, stream, stages);
+  } else {
+    // float32 with a gate: the gate rows form the attention's upstream gradient and
+    // delta in the workspace; the attention stages then read that gradient.
+    const mimir::BwdWorkspace ws = mimir::bwd_workspace_layout(
+        p->total_tokens, p->num_q_heads, p->numseqs, p->max_seqlen_all,
+        (size_t)p->total_tokens * p->num_q_heads * D * sizeof(float));
+    float* const dout_s = (float*)((char*)p->workspace + ws.dout);
+    e = mimir::launch_prologue(pro, stream);
+    if (e == hipSuccess && (stages & MIMIR_BWD_STAGE_DELTA))
+      e = mimir::launch_gate_bwd_f32(*p, dout_s, (float*)((char*)p->workspace + ws.delta), stream);
+    if (e == hipSuccess) {
+      MimirPrefixLMBwdParams q = *p;
+      q.dout = dout_s;
+      q.dout_stride_token = (int64_t)p->num_q_heads * D;
+      q.dout_stride_head = D;
+      e = mimir_launch_bwd_f32(q, stream, stages & ~MIMIR_BWD_STAGE_DELTA);
+    }
   }
   return hip_status(e, "backward launch");
+}
+
+int mimir_prefixlm_rope(const MimirRopeParams* p, void* stream) {
+  g_last_error.clear();
+  if (p == nullptr) return fail(MIMIR_ERR_INVALID_ARGUMENT, "params is NULL");
+  if (p->dtype != MIMIR_DTYPE_FLOAT32 && p->dtype != MIMIR_DTYPE_BFLOAT16)
+    return fail(MIMIR_ERR_UNSUPPORTED_DTYPE, "RoPE supports float32 and bfloat16 tensors only (dtype code " +
+                                                 std::to_string(p->dtype) + ")");
+  if (p->total_tokens < 0 || p->num_heads <= 0 || p->head_dim <= 0)
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "negative size or non-positive heads / head_dim");
+  const int vec = p->dtype == MIMIR_DTYPE_FLOAT32 ? 4 : 8;  // elements per 16-byte access
+  if (p->head_dim % (2 * vec) != 0)
+    return fail(MIMIR_ERR_UNSUPPORTED_SHAPE, "RoPE head_dim " + std::to_string(p->head_dim) + " must be a multiple of " +
+                                                 std::to_string(2 * vec) + " for this dtype");
+  if (p->total_tokens == 0) return MIMIR_OK;
+  if (p->x == nullptr || p->y == nullptr || p->cos == nullptr || p->sin == nullptr)
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "RoPE tensor pointer is NULL");
+  if (!aligned16(p->x) || !aligned16(p->y) || !aligned16(p->cos) || !aligned16(p->sin) ||
+      p->x_stride_token % vec || p->x_stride_head % vec || p->y_stride_token % vec || p->y_stride_head % vec ||
+      p->cs_stride_token % 4)
+    return fail(MIMIR_ERR_UNSUPPORTED_SHAPE,
+                "RoPE tensors must be 16-byte aligned with strides that are multiples of 16 bytes");
+  if (p->cs_stride_token < p->head_dim || p->x_stride_head < 0 || p->y_stride_head < 0)
+    return fail(MIMIR_ERR_UNSUPPORTED_SHAPE, "RoPE rows overlap");
+  return hip_status(mimir::launch_rope(*p, (hipStream_t)stream), "RoPE launch");
 }
 
 }  // extern "C"

@@ -144,6 +144,13 @@ __device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
 
 __device__ __forceinline__ bf16x8 to_bf16x8(f32x8 v) { return __builtin_convertvector(v, bf16x8); }
 
+// Element-type rounding of an fp32 value (round to nearest even for bf16).
+__device__ __forceinline__ float round_to(float x, bf16_t) { return (float)(bf16_t)x; }
+__device__ __forceinline__ float round_to(float x, float) { return x; }
+// Logistic sigmoid in fp32, 1 / (1 + exp(-x)), the formula torch evaluates
+// (in fp32 for bf16 tensors) for torch.sigmoid.
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+
 // ---------------------------------------------------------------------------
 // LDS tile layout.  A [64][D] bf16 operand tile is stored with
 //   * a row stride of D/8 + 1 sixteen-byte units (one unit of padding), and
@@ -307,13 +314,18 @@ constexpr int kSplitPairHeads = 384;              // most (pair, kv head) combin
 constexpr int kSplitSlotFloats = 2 * 128 * 128;   // dK + dV partial of one part
 
 // Backward workspace sections (byte offsets, 256-byte aligned).
+// `dout_bytes`: the gated backward's upstream-gradient buffer (0 without a gate).
 struct BwdWorkspace {
-  size_t delta, lse2, plan_q, plan_k, counters, slots, total;
+  size_t delta, lse2, plan_q, plan_k, counters, slots, dout, total;
   int cap_q, cap_k, pair_heads;
 };
-BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all);
+BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all,
+                                  size_t dout_bytes = 0);
 
 // delta[h, t] = sum_d O[t, h, d] * dO[t, h, d] and lse2[h, t] = lse[h, t] * log2(e), bf16 O / dO.
+// With a gate, `dout` is the gradient of the gated output: the rows also form
+// the attention's upstream gradient dout_s = round(dout * s) (which delta then
+// uses) and dgate = round(round(dout * O) * (1 - s) * s), s = round(sigmoid(gate)).
 struct DeltaArgs {
   const bf16_t* o;
   const bf16_t* dout;
@@ -322,6 +334,10 @@ struct DeltaArgs {
   float* lse2;
   int64_t o_st, o_sh, do_st, do_sh, lse_sh;
   int T, Hq, D;
+  const bf16_t* gate;  // NULL: no gate
+  bf16_t* dgate;
+  bf16_t* dout_s;
+  int64_t g_st, g_sh, dg_st, dg_sh, ds_st, ds_sh;
 };
 
 // Zero the rows of one [T, H, D] tensor (and lse = -inf if non-NULL) that lie
@@ -351,6 +367,12 @@ int device_cu_count();
 FillArgs fill_args(void* x, int64_t st, int64_t sh, float* lse, int64_t lse_sh, const int32_t* cu, int numseqs,
                    int total_seqlen, int T, int H, int D, int elem_bytes);
 hipError_t launch_prologue(const Prologue& pro, hipStream_t stream);
+
+// Layer kernels (prefixlm_layer.hip).
+hipError_t launch_rope(const MimirRopeParams& p, hipStream_t stream);
+hipError_t launch_gate_fwd_f32(const MimirPrefixLMFwdParams& p, hipStream_t stream);
+// float32 gate backward rows: dout_s = dout * s, delta, dgate (one thread per row).
+hipError_t launch_gate_bwd_f32(const MimirPrefixLMBwdParams& p, float* dout_s, float* delta, hipStream_t stream);
 }  // namespace mimir
 
 // Internal launchers (implemented per kernel file, dispatched from prefixlm_capi.hip).

@@ -47,10 +47,13 @@ struct FwdArgs {
   const int2* plan;  // (sequence, query tile) per workgroup row, heaviest first (prefixlm_prologue.hip)
   float scale;       // softmax scale
   float scale_log2;  // softmax scale * log2(e)
+  const bf16_t* gate;  // optional sigmoid output gate [T, Hq, D]; y = round(round(sigmoid(gate)) * O)
+  bf16_t* y;
+  int64_t g_st, g_sh, y_st, y_sh;
 };
 
-template <int D>
-__global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) {
+template <int D, int kGated>
+__device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   constexpr int DT = D / 32;  // 32-row d tiles of O^T
   constexpr int KS = D / 16;  // k-steps of S^T = K Q^T
 
@@ -243,9 +246,41 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) 
         for (int e = 0; e < 4; ++e) t[e] = oacc[dt][4 * rg + e] * inv;
         *(bf16x4*)&orow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
       }
+    if constexpr (kGated != 0) {
+      // Sigmoid output gate in the store (layers.py:239): y = round(s * O) with
+      // s = round(sigmoid(gate)) and O the rounded attention output, as the
+      // reference's bf16 torch.sigmoid(gate) * attn_output rounds them.
+      const bf16_t* grow = a.gate + (int64_t)(g.start + qpos) * a.g_st + (int64_t)h * a.g_sh;
+      bf16_t* yrow = a.y + (int64_t)(g.start + qpos) * a.y_st + (int64_t)h * a.y_sh;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int col = 32 * dt + 8 * rg + 4 * hi;
+          const bf16x4 gv = *(const bf16x4*)&grow[col];
+          f32x4 t;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float ob = round_to(oacc[dt][4 * rg + e] * inv, bf16_t());
+            t[e] = round_to(sigmoid_f32((float)gv[e]), bf16_t()) * ob;
+          }
+          *(bf16x4*)&yrow[col] = __builtin_convertvector(t, bf16x4);
+        }
+    }
     if (hi == 0 && a.lse != nullptr)
       a.lse[(int64_t)h * a.lse_sh + g.start + qpos] = m_run * a.scale + fast_log2(l_tot) * kLn2;
   }
+}
+
+// Plain and gated stores are separate kernels, so that the gate's pointers stay
+// out of the plain kernel's scalar registers.
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) {
+  fwd_body<D, 0>(a);
+}
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void fwd_bf16_gated_kernel(const FwdArgs a) {
+  fwd_body<D, 1>(a);
 }
 
 template <int D>
@@ -270,6 +305,10 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t str
   a.is_causal = p.is_causal;
   a.scale = p.softmax_scale;
   a.scale_log2 = p.softmax_scale * kLog2e;
+  a.gate = (const bf16_t*)p.gate;
+  a.y = (bf16_t*)p.gated_out;
+  a.g_st = p.gate_stride_token; a.g_sh = p.gate_stride_head;
+  a.y_st = p.gated_out_stride_token; a.y_sh = p.gated_out_stride_head;
   static_assert(kBlockM == kPlanTile, "work-list tiles are the forward's query tiles");
   const int cap = plan_capacity(p.total_tokens, p.numseqs, p.max_seqlen_all);
   int2* plan = (int2*)p.workspace;
@@ -280,8 +319,12 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t str
   hipError_t e = launch_prologue(pro, stream);
   if (e != hipSuccess || cap == 0) return e;
   // workgroup r * Hq + h: list entry r, head h (the heads of one tile back to back)
-  hipLaunchKernelGGL(fwd_bf16_kernel<D>, dim3((unsigned)cap * (unsigned)p.num_q_heads), dim3(kThreads), 0, stream,
-                     a);
+  if (a.gate != nullptr)
+    hipLaunchKernelGGL(fwd_bf16_gated_kernel<D>, dim3((unsigned)cap * (unsigned)p.num_q_heads), dim3(kThreads), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL(fwd_bf16_kernel<D>, dim3((unsigned)cap * (unsigned)p.num_q_heads), dim3(kThreads), 0,
+                       stream, a);
   return hipGetLastError();
 }
 

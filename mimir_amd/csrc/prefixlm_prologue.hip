@@ -229,13 +229,14 @@ __device__ void plan_block(const PlanArgs& a) {
 // lse2) with one FMA.
 constexpr int kDeltaPasses = 4;
 
-template <int D>
+template <int D, bool kGated>
 __device__ void delta_block(const DeltaArgs& a, int b) {
+#pragma clang fp contract(off)
   constexpr int LPR = D / 8;            // lanes per row
   constexpr int RPP = kThreads / LPR;   // rows per pass
   const int c = threadIdx.x % LPR;
   const int64_t rows = (int64_t)a.T * a.Hq;
-  bf16x8 ov[kDeltaPasses], dv[kDeltaPasses];
+  bf16x8 ov[kDeltaPasses], dv[kDeltaPasses], gv[kDeltaPasses];
   int t[kDeltaPasses], h[kDeltaPasses];
   bool valid[kDeltaPasses];
 #pragma unroll
@@ -247,14 +248,31 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
     if (valid[i]) {
       ov[i] = *(const bf16x8*)&a.o[(int64_t)t[i] * a.o_st + (int64_t)h[i] * a.o_sh + c * 8];
       dv[i] = *(const bf16x8*)&a.dout[(int64_t)t[i] * a.do_st + (int64_t)h[i] * a.do_sh + c * 8];
+      if constexpr (kGated) gv[i] = *(const bf16x8*)&a.gate[(int64_t)t[i] * a.g_st + (int64_t)h[i] * a.g_sh + c * 8];
     }
   }
 #pragma unroll
   for (int i = 0; i < kDeltaPasses; ++i) {
     float acc = 0.f;
     if (valid[i]) {
+      if constexpr (kGated) {
+        bf16x8 ds, dg;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)ov[i][e] * (float)dv[i][e];
+        for (int e = 0; e < 8; ++e) {
+          const float s = round_to(sigmoid_f32((float)gv[i][e]), bf16_t());
+          const float dy = (float)dv[i][e], o = (float)ov[i][e];
+          const float dso = round_to(dy * s, bf16_t());   // the attention's upstream gradient
+          const float dsg = round_to(dy * o, bf16_t());   // gradient of sigmoid(gate)
+          ds[e] = (bf16_t)dso;
+          dg[e] = (bf16_t)(dsg * (1.0f - s) * s);
+          acc += dso * o;
+        }
+        *(bf16x8*)&a.dout_s[(int64_t)t[i] * a.ds_st + (int64_t)h[i] * a.ds_sh + c * 8] = ds;
+        *(bf16x8*)&a.dgate[(int64_t)t[i] * a.dg_st + (int64_t)h[i] * a.dg_sh + c * 8] = dg;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)ov[i][e] * (float)dv[i][e];
+      }
     }
 #pragma unroll
     for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
@@ -287,7 +305,7 @@ __device__ void fill_block(const FillArgs& a, int b) {
   }
 }
 
-template <int kDeltaD>  // 0: no delta rows
+template <int kDeltaD, bool kGated>  // kDeltaD = 0: no delta rows
 __global__ __launch_bounds__(kThreads) void prologue_kernel(const PrologueArgs a) {
   int b = blockIdx.x;
   if (b < a.nplan) {
@@ -297,7 +315,7 @@ __global__ __launch_bounds__(kThreads) void prologue_kernel(const PrologueArgs a
   b -= a.nplan;
   if constexpr (kDeltaD > 0) {
     if (b < a.delta_blocks) {
-      delta_block<kDeltaD>(a.delta, b);
+      delta_block<kDeltaD, kGated>(a.delta, b);
       return;
     }
     b -= a.delta_blocks;
@@ -336,7 +354,8 @@ PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int nu
   return a;
 }
 
-BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all) {
+BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all,
+                                  size_t dout_bytes) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   BwdWorkspace w;
   const size_t rows = (size_t)(total_tokens > 0 ? total_tokens : 0) * (size_t)(num_q_heads > 0 ? num_q_heads : 0);
@@ -350,7 +369,8 @@ BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs
   w.plan_k = align(w.plan_q + (size_t)w.cap_q * sizeof(int2));
   w.counters = align(w.plan_k + (size_t)w.cap_k * sizeof(int4));
   w.slots = align(w.counters + ((size_t)w.pair_heads + 2) * sizeof(int));
-  w.total = w.slots + (size_t)w.pair_heads * 2 * kSplitSlotFloats * sizeof(float);
+  w.dout = align(w.slots + (size_t)w.pair_heads * 2 * kSplitSlotFloats * sizeof(float));
+  w.total = dout_bytes > 0 ? w.dout + dout_bytes : w.slots + (size_t)w.pair_heads * 2 * kSplitSlotFloats * sizeof(float);
   return w;
 }
 
@@ -398,12 +418,15 @@ hipError_t launch_prologue(const Prologue& pro, hipStream_t stream) {
   const int64_t blocks = (int64_t)a.nplan + a.delta_blocks + (int64_t)a.nfill * a.fill_blocks;
   if (blocks == 0) return hipSuccess;
   const dim3 grid((unsigned)blocks), block(kThreads);
+  const bool gated = delta_d > 0 && pro.delta.gate != nullptr;
+  void (*kernel)(PrologueArgs) = nullptr;
   switch (delta_d) {
-    case 0: hipLaunchKernelGGL(prologue_kernel<0>, grid, block, 0, stream, a); break;
-    case 64: hipLaunchKernelGGL(prologue_kernel<64>, grid, block, 0, stream, a); break;
-    case 128: hipLaunchKernelGGL(prologue_kernel<128>, grid, block, 0, stream, a); break;
+    case 0: kernel = prologue_kernel<0, false>; break;
+    case 64: kernel = gated ? prologue_kernel<64, true> : prologue_kernel<64, false>; break;
+    case 128: kernel = gated ? prologue_kernel<128, true> : prologue_kernel<128, false>; break;
     default: return hipErrorInvalidValue;
   }
+  hipLaunchKernelGGL(kernel, grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

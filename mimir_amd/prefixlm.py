@@ -145,11 +145,13 @@ def check_metadata(prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
 
 
 def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
-                softmax_scale):
+                softmax_scale, gate=None, gated_out=None):
     """Validate, allocate O / lse and fill the C parameter struct of the forward.
 
     Returns ``(params, out, lse, keep)``; ``keep`` holds every tensor the struct
-    points to and must outlive the launch.
+    points to and must outlive the launch.  With ``gate`` ([T, Hq, D], the
+    sigmoid output gate of src/mimir/model/layers.py:239) the launch also writes
+    ``gated_out`` (same shape; allocated by the caller, may be a strided view).
     """
     for name, t in (("q", q), ("k", k), ("v", v)):
         _check_device_tensor(name, t)
@@ -175,7 +177,32 @@ def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_
         T, hq, hkv, d, n, _scalar(total_seqlen), max_all, int(bool(is_causal)),
         _DTYPES[q.dtype], float(softmax_scale), ws.data_ptr(), ws_bytes,
     )
-    return p, out, lse, (q, k, v, pl, cl, cu, ws)
+    keep = (q, k, v, pl, cl, cu, ws)
+    if gate is not None:
+        gate = _gate_operand("gate", gate, (T, hq, d), q.dtype)
+        _gate_operand("gated_out", gated_out, (T, hq, d), q.dtype, copy=False)
+        p.gate, p.gate_stride_token, p.gate_stride_head = gate.data_ptr(), gate.stride(0), gate.stride(1)
+        p.gated_out = gated_out.data_ptr()
+        p.gated_out_stride_token, p.gated_out_stride_head = gated_out.stride(0), gated_out.stride(1)
+        keep = keep + (gate, gated_out)
+    return p, out, lse, keep
+
+
+def _gate_operand(name: str, t, shape, dtype, copy: bool = True) -> Tensor:
+    """A gate-side tensor: [T, Hq, D] of the attention's dtype on its device.  Inputs
+    are re-laid out if the kernels cannot read them in place; outputs must already
+    have a unit head_dim stride and 16-byte aligned rows."""
+    if t is None:
+        raise ValueError(f"{name} is required with a gate")
+    _check_device_tensor(name, t)
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    laid = _kernel_layout(t)
+    if laid is not t and not copy:
+        raise ValueError(f"{name} needs a unit head_dim stride and 16-byte aligned rows")
+    return laid
 
 
 def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
@@ -188,10 +215,13 @@ def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_se
 
 
 def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-                max_seqlen_all, softmax_scale):
+                max_seqlen_all, softmax_scale, gate=None, dgate=None, dq=None, dk=None, dv=None):
     """Validate, allocate dQ / dK / dV and the workspace, fill the backward struct.
 
-    Returns ``(params, dq, dk, dv, keep)``.
+    Returns ``(params, dq, dk, dv, keep)``.  With ``gate``, ``dout`` is the
+    gradient of the gated output and ``out`` the ungated attention output; the
+    launch writes ``dgate`` (caller-allocated).  ``dq`` / ``dk`` / ``dv`` may be
+    given as (strided) output views, e.g. slices of a fused gqkv gradient.
     """
     lib = _capi.load()
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout)):
@@ -207,11 +237,17 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
     q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
     out, dout = _kernel_layout(out), _kernel_layout(dout)
     lse = lse.contiguous()
-    dq = torch.empty((T, hq, d), dtype=q.dtype, device=device)
-    dk = torch.empty((T, hkv, d), dtype=q.dtype, device=device)
-    dv = torch.empty((T, hkv, d), dtype=q.dtype, device=device)
-    ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_bytes(T, hq, n, _scalar(max_seqlen_all)))
-    ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
+    dq = torch.empty((T, hq, d), dtype=q.dtype, device=device) if dq is None else _gate_operand(
+        "dq", dq, (T, hq, d), q.dtype, copy=False)
+    dk = torch.empty((T, hkv, d), dtype=q.dtype, device=device) if dk is None else _gate_operand(
+        "dk", dk, (T, hkv, d), q.dtype, copy=False)
+    dv = torch.empty((T, hkv, d), dtype=q.dtype, device=device) if dv is None else _gate_operand(
+        "dv", dv, (T, hkv, d), q.dtype, copy=False)
+    gate_keep = ()
+    if gate is not None:
+        gate = _gate_operand("gate", gate, (T, hq, d), q.dtype)
+        _gate_operand("dgate", dgate, (T, hq, d), q.dtype, copy=False)
+        gate_keep = (gate, dgate)
     p = _capi.BwdParams(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr(), lse.data_ptr(),
         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
@@ -221,9 +257,15 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
         dq.stride(0), dq.stride(1), dk.stride(0), dk.stride(1), dv.stride(0), dv.stride(1),
         lse.stride(0),
         T, hq, hkv, d, n, _scalar(total_seqlen), _scalar(max_seqlen_all), int(bool(is_causal)),
-        _DTYPES[q.dtype], float(softmax_scale), ws.data_ptr(), ws_bytes,
+        _DTYPES[q.dtype], float(softmax_scale), 0, 0,
     )
-    return p, dq, dk, dv, (q, k, v, out, dout, lse, pl, cl, cu, ws)
+    if gate is not None:
+        p.gate, p.gate_stride_token, p.gate_stride_head = gate.data_ptr(), gate.stride(0), gate.stride(1)
+        p.dgate, p.dgate_stride_token, p.dgate_stride_head = dgate.data_ptr(), dgate.stride(0), dgate.stride(1)
+    ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p)))
+    ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
+    return p, dq, dk, dv, (q, k, v, out, dout, lse, pl, cl, cu, ws) + gate_keep
 
 
 def _bwd_impl(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
