@@ -159,6 +159,93 @@ def copy_calibration(torch, dev, mib: int, reps: int) -> int:
     return 0
 
 
+def layer_bench(torch, dev, args) -> int:
+    """The attention layer core of src/mimir/model/layers.py:182-239 on a workload's shapes.
+
+    fused:   mimir_amd.layer.gated_attention (RoPE kernel on q / k, gate in the
+             attention store and its backward in the delta rows, one gqkv gradient)
+    unfused: the reference's composition -- split views, fp32 torch RoPE
+             (layers.py:24-40), the same prefix-LM operator, torch.sigmoid(gate) * attn
+    Both run forward + backward from the gqkv projection output to the o_proj input.
+    The RoPE kernel is also timed alone against the HBM roofline (bytes: q read and
+    written, cos / sin read).  Prints one JSON line.
+    """
+    from mimir_amd import flash_attn_varlen_prefixlm
+    from mimir_amd import layer as L
+    from mimir_amd.workloads import CONFIG_NAMES, make_config
+
+    case = make_config(args.workload, seed=args.seed)
+    c = case.to(dev)
+    T, hq, d = case.q.shape
+    hkv = case.k.shape[1]
+    dt = case.q.dtype
+    gen = torch.Generator().manual_seed(args.seed + 1)
+    gqkv = torch.randn(T, (2 * hq + 2 * hkv) * d, generator=gen).to(dt).to(dev)
+    dy = torch.randn(T, hq * d, generator=gen).to(dt).to(dev)
+    pos = torch.cat([torch.arange(n) for n in case.seq_lens] + [torch.zeros(T - sum(case.seq_lens), dtype=torch.int64)])
+    inv_freq = 1.0 / (10000.0 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    emb = torch.cat((torch.outer(pos.float(), inv_freq),) * 2, dim=-1)
+    cos, sin = emb.cos().to(dev), emb.sin().to(dev)
+    meta = dict(prefix_lens=c.prefix_lens, causal_lens=c.causal_lens, cu_seqlens=c.cu_seqlens,
+                total_seqlen=c.total_seqlen, numseqs=c.numseqs, max_seqlen_all=c.max_seqlen_all)
+
+    def rope_torch(x):
+        x1, x2 = x[..., : d // 2], x[..., d // 2:]
+        return ((x * cos.unsqueeze(-2)) + (torch.cat((-x2, x1), dim=-1) * sin.unsqueeze(-2))).to(x.dtype)
+
+    def fused():
+        g = gqkv.detach().requires_grad_(True)
+        L.gated_attention(g, (cos, sin), hq, hkv, case.is_causal, **meta).backward(dy)
+
+    def unfused():
+        g = gqkv.detach().requires_grad_(True)
+        gate, q, k, v = g.view(T, 2 * hq + 2 * hkv, d).split((hq, hq, hkv, hkv), dim=1)
+        attn = flash_attn_varlen_prefixlm(rope_torch(q), rope_torch(k), v, case.is_causal,
+                                          max_seqlen_prefix=c.max_seqlen_prefix,
+                                          max_seqlen_causal=c.max_seqlen_causal, **meta)
+        (torch.sigmoid(gate) * attn).reshape(T, hq * d).backward(dy)
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    K, W = max(1, args.steps), max(1, args.warmup)
+    ms_fused = timed(fused, K, W)
+    ms_unfused = timed(unfused, K, W)
+    qv = gqkv.view(T, 2 * hq + 2 * hkv, d)[:, hq:2 * hq]
+    out = torch.empty((T, hq, d), dtype=dt, device=dev)
+    ms_rope = timed(lambda: L.rope(qv, cos, sin, out=out), 4 * K, W)
+    rope_bytes = 2 * T * hq * d * gqkv.element_size() + 2 * T * d * 4
+    rope_gbs = rope_bytes / (ms_rope * 1e-3) / 1e9
+    res = {
+        "metric": "attention layer core (split, RoPE, prefix-LM attention, sigmoid gate) fwd+bwd ms",
+        "value": round(ms_fused, 4),
+        "unit": "ms",
+        "higher_is_better": False,
+        "steps": K,
+        "warmup": W,
+        "dtype": "bf16" if dt == torch.bfloat16 else "fp32",
+        "data": "synthetic",
+        "config": {"workload": CONFIG_NAMES[args.workload], "tokens": T, "q_heads": hq, "kv_heads": hkv,
+                   "head_dim": d, "gqkv_shape": [T, (2 * hq + 2 * hkv) * d], "seed": args.seed},
+        "unfused_ms": round(ms_unfused, 4),
+        "speedup_vs_unfused": round(ms_unfused / ms_fused, 3),
+        "rope": {"kernel": "rope_kernel", "ms": round(ms_rope, 5), "bound": "hbm", "achieved": round(rope_gbs, 1),
+                 "peak": HBM_GBS, "unit": "GB/s", "frac": round(rope_gbs / HBM_GBS, 4),
+                 "bytes_per_launch": rope_bytes},
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -167,6 +254,10 @@ def main() -> int:
     ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layer", action="store_true",
+                    help="instead of the operator, time the attention layer core (gqkv split, RoPE, attention, "
+                         "sigmoid gate; fwd+bwd) fused (mimir_amd.layer) against the reference's composition of "
+                         "torch ops around the same operator")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="instead of the step, time a plain device copy of this many MiB (reference kernel of known "
                          "HBM traffic for scaling the FETCH_SIZE / WRITE_SIZE counters)")
@@ -189,6 +280,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.copy_calibration_mib > 0:
         return copy_calibration(torch, dev, args.copy_calibration_mib, max(1, args.steps))
+    if args.layer:
+        return layer_bench(torch, dev, args)
     case = make_config(args.workload, seed=args.seed)
     c = case.to(dev)
     T, hq, d = c.q.shape

@@ -150,6 +150,12 @@ __device__ __forceinline__ float round_to(float x, float) { return x; }
 // Logistic sigmoid in fp32, 1 / (1 + exp(-x)), the formula torch evaluates
 // (in fp32 for bf16 tensors) for torch.sigmoid.
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+// The same with the hardware exp2 and reciprocal (about 1 ulp each): for values
+// that are rounded to bf16 right after, where the difference to sigmoid_f32
+// changes a result only when it lies within ~2^-22 of a bf16 rounding boundary.
+__device__ __forceinline__ float sigmoid_bf16(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + fast_exp2(-x * kLog2e));
+}
 
 // ---------------------------------------------------------------------------
 // LDS tile layout.  A [64][D] bf16 operand tile is stored with

@@ -120,6 +120,24 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
     const uint32_t off = (uint32_t)(((int64_t)qpos * a.q_st + 16 * ks + 8 * hi) * 2);
     qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, off));
   }
+  // Gated store: round(sigmoid(gate)) of this lane's output elements, formed
+  // before the tile loop so that neither the gate rows' latency nor the
+  // sigmoid lands in the epilogue (rows >= nq read as 0 and are not stored).
+  bf16x4 sgate[kGated ? DT * 4 : 1];
+  if constexpr (kGated != 0) {
+    const __amdgpu_buffer_rsrc_t rgate =
+        make_rsrc(a.gate + (int64_t)g.start * a.g_st + (int64_t)h * a.g_sh, rows_bytes(g.nq, a.g_st, D));
+#pragma unroll
+    for (int i = 0; i < DT * 4; ++i) {
+      const int col = 32 * (i >> 2) + 8 * (i & 3) + 4 * hi;
+      const uint32_t off = (uint32_t)(((int64_t)qpos * a.g_st + col) * 2);
+      const bf16x4 gv = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rgate, off, 0, 0));
+      f32x4 sv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sv[e] = sigmoid_bf16((float)gv[e]);
+      sgate[i] = __builtin_convertvector(sv, bf16x4);
+    }
+  }
 
   f32x16 oacc[DT];
 #pragma unroll
@@ -250,21 +268,16 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
       // Sigmoid output gate in the store (layers.py:239): y = round(s * O) with
       // s = round(sigmoid(gate)) and O the rounded attention output, as the
       // reference's bf16 torch.sigmoid(gate) * attn_output rounds them.
-      const bf16_t* grow = a.gate + (int64_t)(g.start + qpos) * a.g_st + (int64_t)h * a.g_sh;
       bf16_t* yrow = a.y + (int64_t)(g.start + qpos) * a.y_st + (int64_t)h * a.y_sh;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
-          const int col = 32 * dt + 8 * rg + 4 * hi;
-          const bf16x4 gv = *(const bf16x4*)&grow[col];
           f32x4 t;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float ob = round_to(oacc[dt][4 * rg + e] * inv, bf16_t());
-            t[e] = round_to(sigmoid_f32((float)gv[e]), bf16_t()) * ob;
-          }
-          *(bf16x4*)&yrow[col] = __builtin_convertvector(t, bf16x4);
+          for (int e = 0; e < 4; ++e)
+            t[e] = (float)sgate[4 * dt + rg][e] * round_to(oacc[dt][4 * rg + e] * inv, bf16_t());
+          *(bf16x4*)&yrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
         }
     }
     if (hi == 0 && a.lse != nullptr)

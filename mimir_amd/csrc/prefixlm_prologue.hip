@@ -259,7 +259,7 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
         bf16x8 ds, dg;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float s = round_to(sigmoid_f32((float)gv[i][e]), bf16_t());
+          const float s = round_to(sigmoid_bf16((float)gv[i][e]), bf16_t());
           const float dy = (float)dv[i][e], o = (float)ov[i][e];
           const float dso = round_to(dy * s, bf16_t());   // the attention's upstream gradient
           const float dsg = round_to(dy * o, bf16_t());   // gradient of sigmoid(gate)
