@@ -109,6 +109,19 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   }
   hipError_t e = launch_prologue(pro, stream);
   if (e != hipSuccess) return e;
+  // dK/dV (head_dim 128) runs as one persistent workgroup per CU; dQ, launched
+  // behind it on a second stream, takes over each CU as its dK/dV workgroup
+  // finishes and so fills the dK/dV tail.  The join makes `stream` wait for both.
+  const bool both = D == 128 && (stages & MIMIR_BWD_STAGE_DKDV) && (stages & MIMIR_BWD_STAGE_DQ);
+  SideStream* ss = both ? side_stream() : nullptr;
+  if (ss != nullptr) {
+    if ((e = hipEventRecord(ss->fork, stream)) != hipSuccess) return e;
+    if ((e = hipStreamWaitEvent(ss->stream, ss->fork, 0)) != hipSuccess) return e;
+    if ((e = launch_bwd_dkdv_pair_bf16(a, p.numseqs, p.max_seqlen_all, stream)) != hipSuccess) return e;
+    if ((e = launch_bwd_dq_bf16(a, D, p.numseqs, p.max_seqlen_all, ss->stream)) != hipSuccess) return e;
+    if ((e = hipEventRecord(ss->join, ss->stream)) != hipSuccess) return e;
+    return hipStreamWaitEvent(stream, ss->join, 0);
+  }
   if (stages & MIMIR_BWD_STAGE_DKDV) {
     e = D == 128 ? launch_bwd_dkdv_pair_bf16(a, p.numseqs, p.max_seqlen_all, stream)
                  : launch_bwd_dkdv_bf16(a, D, p.numseqs, p.max_seqlen_all, stream);

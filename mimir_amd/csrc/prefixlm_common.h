@@ -370,6 +370,14 @@ PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int nu
                    int is_causal, int total_tokens, int kind, int group, int cap, void* items);
 // Compute units of the current device (cached per device).
 int device_cu_count();
+
+// A second stream of the current device with fork / join events (created once
+// per host thread and device, default priority), or nullptr if that failed.
+struct SideStream {
+  hipStream_t stream;
+  hipEvent_t fork, join;
+};
+SideStream* side_stream();
 FillArgs fill_args(void* x, int64_t st, int64_t sh, float* lse, int64_t lse_sh, const int32_t* cu, int numseqs,
                    int total_seqlen, int T, int H, int D, int elem_bytes);
 hipError_t launch_prologue(const Prologue& pro, hipStream_t stream);

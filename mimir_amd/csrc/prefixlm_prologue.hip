@@ -374,6 +374,24 @@ BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs
   return w;
 }
 
+SideStream* side_stream() {
+  constexpr int kMaxDevices = 64;
+  thread_local SideStream side[kMaxDevices];
+  thread_local bool ready[kMaxDevices] = {false};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (!ready[dev]) {
+    SideStream ss;
+    if (hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess)
+      return nullptr;
+    side[dev] = ss;
+    ready[dev] = true;
+  }
+  return &side[dev];
+}
+
 int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
