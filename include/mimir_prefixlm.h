@@ -219,6 +219,52 @@ typedef struct MimirRopeParams {
 } MimirRopeParams;
 int mimir_prefixlm_rope(const MimirRopeParams* params, void* stream);
 
+/* Attention against a static KV cache, the inference path of Mimir2's
+ * Attention (reference: src/mimir/model/layers.py:134-167, _attention_with_cache,
+ * with the Cache of layers.py:107-115).  For batch row b (cache row
+ * r = batch_indices ? batch_indices[b] : b) and c = cache_lengths[b]:
+ *
+ *   1. k_new / v_new [b, i] are written to cache_k / cache_v [r, c + i], i < S;
+ *   2. query i of q [b, i, h] attends the cache keys j < c + S of kv head
+ *      h / (Hq / Hkv), and if `causal` only j <= c + i (the reference's mask);
+ *      softmax scale `softmax_scale`, out [b, i, h] in the element type.
+ *
+ * c + S must not exceed cache_len (the reference raises IndexError there; this
+ * entry point skips the cache writes and keys beyond the cache instead).
+ * max_kv_len is an upper bound of max_b(c + S) (the reference's
+ * kv_len.max().item(), layers.py:143) that sizes the key split.  bf16 only,
+ * head_dim 64 or 128.  The workspace holds the split partial results. */
+typedef struct MimirCacheAttnParams {
+  const void* q;              /* [B, S, Hq, D] */
+  const void* k_new;          /* [B, S, Hkv, D] */
+  const void* v_new;          /* [B, S, Hkv, D] */
+  void* cache_k;              /* [>= rows, cache_len, Hkv, D] */
+  void* cache_v;              /* [>= rows, cache_len, Hkv, D] */
+  void* out;                  /* [B, S, Hq, D] */
+  const int32_t* cache_lengths;   /* device int32 [B] */
+  const int32_t* batch_indices;   /* device int32 [B] or NULL (row b) */
+  int64_t q_stride_batch, q_stride_token, q_stride_head;
+  int64_t kn_stride_batch, kn_stride_token, kn_stride_head;
+  int64_t vn_stride_batch, vn_stride_token, vn_stride_head;
+  int64_t ck_stride_batch, ck_stride_token, ck_stride_head;
+  int64_t cv_stride_batch, cv_stride_token, cv_stride_head;
+  int64_t out_stride_batch, out_stride_token, out_stride_head;
+  int32_t batch;              /* B */
+  int32_t seqlen;             /* S (1 for decode) */
+  int32_t cache_len;          /* positions per cache row */
+  int32_t max_kv_len;         /* upper bound of max_b(cache_lengths[b] + S) */
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t causal;
+  int32_t dtype;              /* MIMIR_DTYPE_BFLOAT16 */
+  float softmax_scale;
+  void* workspace;            /* >= mimir_prefixlm_cache_attn_workspace_bytes(params) */
+  size_t workspace_bytes;
+} MimirCacheAttnParams;
+size_t mimir_prefixlm_cache_attn_workspace_bytes(const MimirCacheAttnParams* params);
+int mimir_prefixlm_cache_attn(const MimirCacheAttnParams* params, void* stream);
+
 /* Device-side metadata check: writes to *bad_seq (device int32) the first s in
  * [0, numseqs) with prefix_lens[s] + causal_lens[s] != cu_seqlens[s+1] - cu_seqlens[s]
  * or a negative length, or -1 if none.  The reference raises ValueError for this

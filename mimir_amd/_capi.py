@@ -83,6 +83,22 @@ class RopeParams(ctypes.Structure):
     ]
 
 
+class CacheAttnParams(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp), ("k_new", _vp), ("v_new", _vp), ("cache_k", _vp), ("cache_v", _vp), ("out", _vp),
+        ("cache_lengths", _vp), ("batch_indices", _vp),
+        ("q_stride_batch", _i64), ("q_stride_token", _i64), ("q_stride_head", _i64),
+        ("kn_stride_batch", _i64), ("kn_stride_token", _i64), ("kn_stride_head", _i64),
+        ("vn_stride_batch", _i64), ("vn_stride_token", _i64), ("vn_stride_head", _i64),
+        ("ck_stride_batch", _i64), ("ck_stride_token", _i64), ("ck_stride_head", _i64),
+        ("cv_stride_batch", _i64), ("cv_stride_token", _i64), ("cv_stride_head", _i64),
+        ("out_stride_batch", _i64), ("out_stride_token", _i64), ("out_stride_head", _i64),
+        ("batch", _i32), ("seqlen", _i32), ("cache_len", _i32), ("max_kv_len", _i32),
+        ("num_q_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32), ("causal", _i32), ("dtype", _i32),
+        ("softmax_scale", ctypes.c_float), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 BWD_STAGE_DELTA = 1
 BWD_STAGE_DKDV = 2
 BWD_STAGE_DQ = 4
@@ -97,6 +113,8 @@ EXPORTED_SYMBOLS = (
     "mimir_prefixlm_bwd_workspace_bytes",
     "mimir_prefixlm_bwd_workspace_size",
     "mimir_prefixlm_rope",
+    "mimir_prefixlm_cache_attn",
+    "mimir_prefixlm_cache_attn_workspace_bytes",
     "mimir_prefixlm_check_metadata",
     "mimir_prefixlm_last_error",
     "mimir_prefixlm_abi_version",
@@ -138,6 +156,10 @@ def load() -> ctypes.CDLL:
         lib.mimir_prefixlm_bwd_workspace_size.restype = ctypes.c_size_t
         lib.mimir_prefixlm_rope.argtypes = [ctypes.POINTER(RopeParams), _vp]
         lib.mimir_prefixlm_rope.restype = ctypes.c_int
+        lib.mimir_prefixlm_cache_attn.argtypes = [ctypes.POINTER(CacheAttnParams), _vp]
+        lib.mimir_prefixlm_cache_attn.restype = ctypes.c_int
+        lib.mimir_prefixlm_cache_attn_workspace_bytes.argtypes = [ctypes.POINTER(CacheAttnParams)]
+        lib.mimir_prefixlm_cache_attn_workspace_bytes.restype = ctypes.c_size_t
         lib.mimir_prefixlm_check_metadata.argtypes = [_vp, _vp, _vp, _i32, _vp, _vp]
         lib.mimir_prefixlm_check_metadata.restype = ctypes.c_int
         lib.mimir_prefixlm_last_error.argtypes = []

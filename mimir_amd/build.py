@@ -47,6 +47,7 @@ SOURCES = [
     "prefixlm_f32.hip",
     "prefixlm_prologue.hip",
     "prefixlm_layer.hip",
+    "prefixlm_cache_bf16.hip",
 ]
 
 

@@ -1,0 +1,393 @@
+// Attention against a static KV cache (inference), bf16, for gfx950 (MI355X).
+//
+// Reference: src/mimir/model/layers.py:134-167 (_attention_with_cache).  The
+// new keys / values go into the cache at positions cache_lengths[b] + i, then
+// every query row attends the cache keys j < kv_len = cache_lengths[b] + S
+// (and j <= cache_lengths[b] + i when causal).  The reference materializes the
+// repeated K/V heads and a [B, S, max_kv_len] mask for SDPA; here:
+//
+//   cache_append_kernel   the scatter of k_new / v_new into the cache rows
+//   cache_attn_kernel     one workgroup per (batch row, kv head, 128 query rows,
+//                         key split): the G query heads of a kv head share its
+//                         K / V tiles (rows are (token, head) pairs, token-major),
+//                         64-key tiles stream through two LDS stages, S^T = K Q^T
+//                         and O^T += V^T P^T on bf16 MFMA with an online softmax
+//                         (the forward kernel's arithmetic)
+//   cache_combine_kernel  merges the key splits' partial (max, sum, O) rows
+//
+// Decode (S = 1) has only G rows per kv head, so the key range is split over
+// enough workgroups to cover the chip (flash-decoding); the kernel is then
+// bound by the HBM read of the cache.  Prefill with a long S fills the row
+// tiles and runs on the MFMA like the forward kernel.
+#include "prefixlm_common.h"
+
+namespace mimir {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRows = kWaves * 32;  // query rows per workgroup
+constexpr int kKeys = 64;           // keys per tile
+
+struct CacheArgs {
+  const bf16_t* q;
+  const bf16_t* kn;
+  const bf16_t* vn;
+  bf16_t* ck;
+  bf16_t* cv;
+  bf16_t* out;
+  const int32_t* cache_lengths;
+  const int32_t* batch_indices;
+  int64_t q_sb, q_st, q_sh, kn_sb, kn_st, kn_sh, vn_sb, vn_st, vn_sh;
+  int64_t ck_sb, ck_st, ck_sh, cv_sb, cv_st, cv_sh, o_sb, o_st, o_sh;
+  int B, S, L, Hkv, G, causal, D;
+  int n_rt;        // row tiles per (batch row, kv head)
+  int splits;      // key splits per row tile
+  int split_keys;  // keys per split, a multiple of kKeys
+  float scale_log2;
+  float* part_o;   // [unit, kRows, D] unnormalized O of each split (splits > 1)
+  float* part_ml;  // [unit, kRows, 2]: running max (exp2 domain) and sum
+};
+
+__device__ __forceinline__ int cache_row(const CacheArgs& a, int b) {
+  return a.batch_indices != nullptr ? a.batch_indices[b] : b;
+}
+__device__ __forceinline__ int clamp_len(int c, int L) { return c < 0 ? 0 : (c > L ? L : c); }
+
+// k_new / v_new [b, i, h] -> cache [row(b), cache_lengths[b] + i, h]; 16 bytes per thread.
+__global__ __launch_bounds__(256) void cache_append_kernel(const CacheArgs a) {
+  const int chunks = a.D / 8;
+  const int64_t total = (int64_t)a.B * a.S * a.Hkv * chunks;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+    const int c = (int)(idx % chunks);
+    int64_t t = idx / chunks;
+    const int h = (int)(t % a.Hkv);
+    t /= a.Hkv;
+    const int i = (int)(t % a.S);
+    const int b = (int)(t / a.S);
+    const int pos = a.cache_lengths[b] + i;
+    if (pos < 0 || pos >= a.L) continue;  // beyond the cache: dropped
+    const int64_t r = cache_row(a, b);
+    *(bf16x8*)&a.ck[r * a.ck_sb + (int64_t)pos * a.ck_st + (int64_t)h * a.ck_sh + c * 8] =
+        *(const bf16x8*)&a.kn[(int64_t)b * a.kn_sb + (int64_t)i * a.kn_st + (int64_t)h * a.kn_sh + c * 8];
+    *(bf16x8*)&a.cv[r * a.cv_sb + (int64_t)pos * a.cv_st + (int64_t)h * a.cv_sh + c * 8] =
+        *(const bf16x8*)&a.vn[(int64_t)b * a.vn_sb + (int64_t)i * a.vn_st + (int64_t)h * a.vn_sh + c * 8];
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs a) {
+  constexpr int DT = D / 32;
+  constexpr int KS = D / 16;
+  using L = TileLayout<D>;
+  __shared__ __attribute__((aligned(16))) bf16_t sK0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sK1[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV1[L::kElems];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hi = lane >> 5;
+
+  int u = blockIdx.x;
+  const int split = u % a.splits;
+  u /= a.splits;
+  const int rt = u % a.n_rt;
+  u /= a.n_rt;
+  const int hk = u % a.Hkv;
+  const int b = u / a.Hkv;
+
+  const int clen = clamp_len(a.cache_lengths[b], a.L);
+  const int kv = min(clen + a.S, a.L);  // keys of this batch row
+  const int k0 = split * a.split_keys;
+  if (k0 >= kv) return;  // the combine reads only the splits that hold keys
+  const int k1 = min(kv, k0 + a.split_keys);
+  const int R = a.S * a.G;  // query rows (token-major (token, head) pairs)
+
+  // This lane's row and its key limit.
+  const int row = rt * kRows + wave * 32 + l32;
+  const bool row_ok = row < R;
+  const int ti = row_ok ? row / a.G : 0;
+  const int h = hk * a.G + (row_ok ? row - ti * a.G : 0);
+  const int kend_lane = row_ok ? (a.causal ? min(clen + ti + 1, kv) : kv) : 0;
+  // Wave-wide bounds (rows are token-major, so the wave's last row has the largest limit).
+  const int r0 = rt * kRows + wave * 32;
+  const bool wave_active = r0 < R;
+  const int r_last = min(r0 + 31, R - 1);
+  const int w_kend_max = wave_active ? (a.causal ? min(clen + r_last / a.G + 1, kv) : kv) : 0;
+  const int w_kend_min = wave_active ? (a.causal ? min(clen + r0 / a.G + 1, kv) : kv) : 0;
+  // Workgroup range of key tiles inside this split.
+  const int wg_r_last = min(rt * kRows + kRows - 1, R - 1);
+  const int wg_kend = a.causal ? min(clen + wg_r_last / a.G + 1, kv) : kv;
+  const int kt0 = k0 / kKeys;
+  const int kt1 = (min(k1, wg_kend) + kKeys - 1) / kKeys;  // may be <= kt0: nothing to attend
+
+  const int64_t crow = cache_row(a, b);
+  const bf16_t* kbase = a.ck + crow * a.ck_sb + (int64_t)hk * a.ck_sh;
+  const bf16_t* vbase = a.cv + crow * a.cv_sb + (int64_t)hk * a.cv_sh;
+  const TileLoader<D, kWaves> ldk(a.ck_st, wave, lane), ldv(a.cv_st, wave, lane);
+  if (kt0 < kt1) {
+    ldk.issue(kbase, kt0 * kKeys, kv, sK0);
+    ldv.issue(vbase, kt0 * kKeys, kv, sV0);
+  }
+
+  // Q^T B-operand fragments: lane holds row `row`, d = 16*ks + 8*hi .. +7 (0 for rows >= R).
+  bf16x8 qf[KS];
+  {
+    const bf16_t* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)ti * a.q_st + (int64_t)h * a.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = row_ok ? *(const bf16x8*)&qrow[16 * ks + 8 * hi] : bf16x8{};
+  }
+
+  f32x16 oacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  const float c2 = a.scale_log2;
+  const TileLanes<D> tl(lane);
+
+  auto compute = [&](int kt, const bf16_t* sK, const bf16_t* sV) {
+    const int kb = kt * kKeys;
+    if (!wave_active || kb >= w_kend_max) return;
+    f32x16 st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      st[mt] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 kf = *(const bf16x8*)&sK[tl.op_base + mt * 32 * L::kRowElems + ks * 16];
+        st[mt] = mfma32(kf, qf[ks], st[mt]);
+      }
+    }
+    if (kb + kKeys > w_kend_min) {
+      __asm__ volatile("");
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kpos = kb + 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
+          if (kpos >= kend_lane) st[mt][r] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
+    mx = xor32_max(mx);
+    // Lazy rescaling, as in the forward kernel: the reference max moves only
+    // when it grows by more than 2^8 in probability terms.
+    const float m_cand = fmaxf(m_run, mx);
+    const bool grow = (m_cand - m_run) * c2 > 8.f;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = grow ? m_cand : m_run;
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2((m_run - m_new) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      m_run = m_new;
+    }
+    const float mb = m_run == -INFINITY ? 0.f : m_run * c2;
+    float lsum = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = fast_exp2(__builtin_fmaf(st[mt][r], c2, -mb));
+        st[mt][r] = pr;
+        lsum += pr;
+      }
+    l_run += lsum;
+    bf16x8 pf[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int mt = kk >> 1, s8 = (kk & 1) * 8;
+      f32x8 t;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t[e] = st[mt][s8 + e];
+      pf[kk] = to_bf16x8(t);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16_t* vp = &sV[tl.tr_base + kk * 16 * L::kRowElems + dt * 32];
+        oacc[dt] = mfma32(cat8(lds_read_tr16(vp), lds_read_tr16(vp + L::kTrSecond)), pf[kk], oacc[dt]);
+      }
+  };
+
+  for (int kt = kt0; kt < kt1; kt += 2) {
+    wait_vmem();
+    __syncthreads();
+    if (kt + 1 < kt1) {
+      ldk.issue(kbase, (kt + 1) * kKeys, kv, sK1);
+      ldv.issue(vbase, (kt + 1) * kKeys, kv, sV1);
+    }
+    compute(kt, sK0, sV0);
+    if (kt + 1 >= kt1) break;
+    wait_vmem();
+    __syncthreads();
+    if (kt + 2 < kt1) {
+      ldk.issue(kbase, (kt + 2) * kKeys, kv, sK0);
+      ldv.issue(vbase, (kt + 2) * kKeys, kv, sV0);
+    }
+    compute(kt + 1, sK1, sV1);
+  }
+
+  if (!wave_active) return;
+  const float l_tot = xor32_sum(l_run);
+  if (a.splits == 1) {
+    if (!row_ok) return;
+    const float inv = 1.f / l_tot;
+    bf16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)ti * a.o_st + (int64_t)h * a.o_sh;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        f32x4 t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = oacc[dt][4 * rg + e] * inv;
+        *(bf16x4*)&orow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
+      }
+    return;
+  }
+  // Partial result of this split: unnormalized O, the max in the exp2 domain
+  // (-inf: no key of this split is allowed for the row) and the sum.
+  const int64_t slot = (int64_t)blockIdx.x * kRows + wave * 32 + l32;
+  float* po = a.part_o + slot * D;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      f32x4 t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = oacc[dt][4 * rg + e];
+      *(f32x4*)&po[32 * dt + 8 * rg + 4 * hi] = t;
+    }
+  if (hi == 0) {
+    a.part_ml[2 * slot] = m_run == -INFINITY ? -INFINITY : m_run * c2;
+    a.part_ml[2 * slot + 1] = l_tot;
+  }
+}
+
+// out row = sum_c O_c * 2^(m_c - M) / sum_c l_c * 2^(m_c - M) over the splits
+// that hold keys of the batch row; 4 columns per thread.
+__global__ __launch_bounds__(256) void cache_combine_kernel(const CacheArgs a) {
+  const int R = a.S * a.G;
+  const int cols = a.D / 4;
+  const int64_t total = (int64_t)a.B * a.Hkv * R * cols;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+    const int c4 = (int)(idx % cols);
+    int64_t t = idx / cols;
+    const int row = (int)(t % R);
+    t /= R;
+    const int hk = (int)(t % a.Hkv);
+    const int b = (int)(t / a.Hkv);
+    const int clen = clamp_len(a.cache_lengths[b], a.L);
+    const int kv = min(clen + a.S, a.L);
+    const int n_valid = min((kv + a.split_keys - 1) / a.split_keys, a.splits);
+    const int rt = row / kRows, rr = row - rt * kRows;
+    const int64_t unit0 = (((int64_t)b * a.Hkv + hk) * a.n_rt + rt) * a.splits;
+    float M = -INFINITY;
+    for (int c = 0; c < n_valid; ++c) M = fmaxf(M, a.part_ml[2 * ((unit0 + c) * kRows + rr)]);
+    float lsum = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    if (M != -INFINITY) {
+      for (int c = 0; c < n_valid; ++c) {
+        const int64_t slot = (unit0 + c) * kRows + rr;
+        const float m = a.part_ml[2 * slot];
+        if (m == -INFINITY) continue;
+        const float w = fast_exp2(m - M);
+        lsum += a.part_ml[2 * slot + 1] * w;
+        const f32x4 pv = *(const f32x4*)&a.part_o[slot * a.D + 4 * c4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] += pv[e] * w;
+      }
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    const int ti = row / a.G;
+    const int h = hk * a.G + (row - ti * a.G);
+    bf16x4 ob;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ob[e] = (bf16_t)(o[e] * inv);
+    *(bf16x4*)&a.out[(int64_t)b * a.o_sb + (int64_t)ti * a.o_st + (int64_t)h * a.o_sh + 4 * c4] = ob;
+  }
+}
+
+unsigned grid_for(int64_t items) {
+  const int64_t blocks = (items + 255) / 256;
+  return (unsigned)(blocks < 16384 ? (blocks > 0 ? blocks : 1) : 16384);
+}
+
+}  // namespace
+
+CacheSplit cache_split(const MimirCacheAttnParams& p) {
+  CacheSplit s;
+  const int G = p.num_kv_heads > 0 ? p.num_q_heads / p.num_kv_heads : 1;
+  const int64_t R = (int64_t)p.seqlen * G;
+  s.n_rt = (int)((R + kRows - 1) / kRows);
+  int max_kv = p.max_kv_len < p.cache_len ? p.max_kv_len : p.cache_len;
+  if (max_kv < 1) max_kv = 1;
+  const int tiles = (max_kv + kKeys - 1) / kKeys;
+  const int64_t base = (int64_t)p.batch * p.num_kv_heads * s.n_rt;
+  const int64_t target = 4 * (int64_t)device_cu_count();  // workgroups to cover the chip
+  int64_t splits = base > 0 ? (target + base - 1) / base : 1;
+  if (splits < 1) splits = 1;
+  if (splits > tiles) splits = tiles;
+  const int tiles_per_split = (int)((tiles + splits - 1) / splits);
+  s.split_keys = tiles_per_split * kKeys;
+  s.splits = (max_kv + s.split_keys - 1) / s.split_keys;
+  s.units = base * s.splits;
+  s.workspace_bytes = s.splits > 1 ? (size_t)s.units * kRows * ((size_t)p.head_dim + 2) * sizeof(float) : 0;
+  return s;
+}
+
+hipError_t launch_cache_attn_bf16(const MimirCacheAttnParams& p, hipStream_t stream) {
+  const CacheSplit sp = cache_split(p);
+  CacheArgs a;
+  a.q = (const bf16_t*)p.q;
+  a.kn = (const bf16_t*)p.k_new;
+  a.vn = (const bf16_t*)p.v_new;
+  a.ck = (bf16_t*)p.cache_k;
+  a.cv = (bf16_t*)p.cache_v;
+  a.out = (bf16_t*)p.out;
+  a.cache_lengths = p.cache_lengths;
+  a.batch_indices = p.batch_indices;
+  a.q_sb = p.q_stride_batch; a.q_st = p.q_stride_token; a.q_sh = p.q_stride_head;
+  a.kn_sb = p.kn_stride_batch; a.kn_st = p.kn_stride_token; a.kn_sh = p.kn_stride_head;
+  a.vn_sb = p.vn_stride_batch; a.vn_st = p.vn_stride_token; a.vn_sh = p.vn_stride_head;
+  a.ck_sb = p.ck_stride_batch; a.ck_st = p.ck_stride_token; a.ck_sh = p.ck_stride_head;
+  a.cv_sb = p.cv_stride_batch; a.cv_st = p.cv_stride_token; a.cv_sh = p.cv_stride_head;
+  a.o_sb = p.out_stride_batch; a.o_st = p.out_stride_token; a.o_sh = p.out_stride_head;
+  a.B = p.batch;
+  a.S = p.seqlen;
+  a.L = p.cache_len;
+  a.Hkv = p.num_kv_heads;
+  a.G = p.num_q_heads / p.num_kv_heads;
+  a.causal = p.causal != 0;
+  a.D = p.head_dim;
+  a.n_rt = sp.n_rt;
+  a.splits = sp.splits;
+  a.split_keys = sp.split_keys;
+  a.scale_log2 = p.softmax_scale * kLog2e;
+  a.part_o = (float*)p.workspace;
+  a.part_ml = a.part_o + (size_t)sp.units * kRows * p.head_dim;
+  if (sp.splits > 1 && p.workspace == nullptr) return hipErrorInvalidValue;
+  const int64_t appends = (int64_t)a.B * a.S * a.Hkv * (a.D / 8);
+  if (appends > 0) hipLaunchKernelGGL(cache_append_kernel, dim3(grid_for(appends)), dim3(256), 0, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || sp.units == 0) return e;
+  if (p.head_dim == 128)
+    hipLaunchKernelGGL(cache_attn_kernel<128>, dim3((unsigned)sp.units), dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(cache_attn_kernel<64>, dim3((unsigned)sp.units), dim3(kThreads), 0, stream, a);
+  if ((e = hipGetLastError()) != hipSuccess || sp.splits == 1) return e;
+  const int64_t combines = (int64_t)a.B * a.Hkv * a.S * a.G * (a.D / 4);
+  hipLaunchKernelGGL(cache_combine_kernel, dim3(grid_for(combines)), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace mimir

@@ -253,6 +253,56 @@ int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* p, int stages, void*
   return hip_status(e, "backward launch");
 }
 
+size_t mimir_prefixlm_cache_attn_workspace_bytes(const MimirCacheAttnParams* p) {
+  if (p == nullptr || p->batch <= 0 || p->seqlen <= 0 || p->num_kv_heads <= 0 || p->num_q_heads <= 0 ||
+      p->cache_len <= 0)
+    return 0;
+  return mimir::cache_split(*p).workspace_bytes;
+}
+
+int mimir_prefixlm_cache_attn(const MimirCacheAttnParams* p, void* stream) {
+  g_last_error.clear();
+  if (p == nullptr) return fail(MIMIR_ERR_INVALID_ARGUMENT, "params is NULL");
+  if (p->dtype != MIMIR_DTYPE_BFLOAT16)
+    return fail(MIMIR_ERR_UNSUPPORTED_DTYPE, "KV-cache attention supports bfloat16 tensors only (dtype code " +
+                                                 std::to_string(p->dtype) + ")");
+  if (p->batch < 0 || p->seqlen < 0 || p->cache_len < 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0)
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "negative size or non-positive head count");
+  if (p->num_q_heads % p->num_kv_heads != 0)
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "Query heads " + std::to_string(p->num_q_heads) +
+                                                " must be divisible by key/value heads " +
+                                                std::to_string(p->num_kv_heads) + ".");
+  if (!mimir_bf16_head_dim_supported(p->head_dim))
+    return fail(MIMIR_ERR_UNSUPPORTED_SHAPE, "head_dim " + std::to_string(p->head_dim) +
+                                                 " is not supported for bfloat16 (supported: 64, 128)");
+  if (!(p->softmax_scale > 0.f) || !std::isfinite(p->softmax_scale))
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "softmax_scale must be positive and finite");
+  if (p->batch == 0 || p->seqlen == 0) return MIMIR_OK;
+  if (p->cache_len == 0) return fail(MIMIR_ERR_INVALID_ARGUMENT, "the cache holds no positions");
+  if (p->cache_lengths == nullptr) return fail(MIMIR_ERR_INVALID_ARGUMENT, "cache_lengths is NULL");
+  const int D = p->head_dim, dt = p->dtype;
+  int rc;
+  // per batch row a [rows, H, D] tensor: the span checks of the packed operands apply per row
+  if ((rc = check_operand("q", p->q, p->q_stride_token, p->q_stride_head, D, dt, p->seqlen))) return rc;
+  if ((rc = check_operand("k_new", p->k_new, p->kn_stride_token, p->kn_stride_head, D, dt, p->seqlen))) return rc;
+  if ((rc = check_operand("v_new", p->v_new, p->vn_stride_token, p->vn_stride_head, D, dt, p->seqlen))) return rc;
+  if ((rc = check_operand("out", p->out, p->out_stride_token, p->out_stride_head, D, dt, p->seqlen))) return rc;
+  if ((rc = check_operand("cache_k", p->cache_k, p->ck_stride_token, p->ck_stride_head, D, dt, p->cache_len)))
+    return rc;
+  if ((rc = check_operand("cache_v", p->cache_v, p->cv_stride_token, p->cv_stride_head, D, dt, p->cache_len)))
+    return rc;
+  const int64_t bs[6] = {p->q_stride_batch, p->kn_stride_batch, p->vn_stride_batch, p->ck_stride_batch,
+                         p->cv_stride_batch, p->out_stride_batch};
+  for (int64_t b : bs)
+    if (b < 0 || b % 8 != 0)
+      return fail(MIMIR_ERR_UNSUPPORTED_SHAPE, "batch strides must be non-negative multiples of 8 elements");
+  const size_t need = mimir_prefixlm_cache_attn_workspace_bytes(p);
+  if (need > 0 && (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace)))
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +
+                                                std::to_string(need) + " bytes");
+  return hip_status(mimir::launch_cache_attn_bf16(*p, (hipStream_t)stream), "KV-cache attention launch");
+}
+
 int mimir_prefixlm_rope(const MimirRopeParams* p, void* stream) {
   g_last_error.clear();
   if (p == nullptr) return fail(MIMIR_ERR_INVALID_ARGUMENT, "params is NULL");

@@ -382,6 +382,15 @@ FillArgs fill_args(void* x, int64_t st, int64_t sh, float* lse, int64_t lse_sh, 
                    int total_seqlen, int T, int H, int D, int elem_bytes);
 hipError_t launch_prologue(const Prologue& pro, hipStream_t stream);
 
+// KV-cache attention (prefixlm_cache_bf16.hip): the key split and its workspace.
+struct CacheSplit {
+  int n_rt, splits, split_keys;
+  int64_t units;
+  size_t workspace_bytes;
+};
+CacheSplit cache_split(const MimirCacheAttnParams& p);
+hipError_t launch_cache_attn_bf16(const MimirCacheAttnParams& p, hipStream_t stream);
+
 // Layer kernels (prefixlm_layer.hip).
 hipError_t launch_rope(const MimirRopeParams& p, hipStream_t stream);
 hipError_t launch_gate_fwd_f32(const MimirPrefixLMFwdParams& p, hipStream_t stream);

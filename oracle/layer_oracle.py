@@ -23,6 +23,9 @@ function                     pinned by
 ``gate_forward``             sigmoid(0) = 1/2; closed form in fp64
 ``gate_backward``            fp64 closed forms dgate = dy*attn*s*(1-s), dattn = dy*s
 ``gated_attention``          fp64 autograd of the composed chain on tiny inputs
+``attention_with_cache``     empty cache == the prefix-LM oracle (causal: p = 0;
+                             bidirectional: p = n); fp64 brute-force loops for
+                             decode and chunked prefill; the cache writes
 ==========================  =======================================================
 """
 
@@ -35,6 +38,7 @@ from oracle.prefixlm_oracle import dense_backward, dense_forward
 
 __all__ = [
     "apply_rotary_pos_emb",
+    "attention_with_cache",
     "gate_backward",
     "gate_forward",
     "gated_attention",
@@ -115,3 +119,36 @@ def gated_attention(gqkv, cos, sin, hq, hkv, is_causal, prefix_lens, causal_lens
     if cos is not None:
         dq, dk = rope_grad(q, cos, sin, dq), rope_grad(k, cos, sin, dk)
     return y, torch.cat((dgate, dq, dk, dv), dim=1)
+
+
+def attention_with_cache(query, key, value, cache_keys, cache_values, cache_lengths, causal,
+                         cache_batch_indices=None):
+    """layers.py:134-167 restated: write key / value into the cache, attend with the
+    reference's float mask (finfo.min where not allowed).  Inputs [B, S, H, D]; the
+    cache tensors are updated in place; the math runs in fp32 (fp64 stays fp64).
+    Returns [B, S, Hq, D] in the query's dtype."""
+    batch_size, seqlen = query.shape[:2]
+    positions = cache_lengths[:, None] + torch.arange(seqlen, dtype=cache_lengths.dtype)
+    rows = torch.arange(batch_size) if cache_batch_indices is None else cache_batch_indices
+    batch_idx = rows[:, None]
+    cache_keys[batch_idx, positions] = key
+    cache_values[batch_idx, positions] = value
+    kv_len = cache_lengths + seqlen
+    max_kv_len = int(kv_len.max().item())
+    keys = cache_keys[rows, :max_kv_len]
+    values = cache_values[rows, :max_kv_len]
+    hq, hkv = query.shape[2], key.shape[2]
+    if hq != hkv:
+        keys = keys.repeat_interleave(hq // hkv, dim=2)
+        values = values.repeat_interleave(hq // hkv, dim=2)
+    acc = torch.float64 if query.dtype == torch.float64 else torch.float32
+    q, k, v = query.transpose(1, 2).to(acc), keys.transpose(1, 2).to(acc), values.transpose(1, 2).to(acc)
+    key_positions = torch.arange(max_kv_len)
+    valid = key_positions[None, :] < kv_len[:, None]
+    if causal:
+        valid = valid[:, None, :] & (key_positions[None, None, :] <= positions[:, :, None])
+    else:
+        valid = valid[:, None, :]
+    mask = torch.zeros((batch_size, seqlen, max_kv_len), dtype=acc).masked_fill(~valid, torch.finfo(acc).min)
+    out = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask[:, None])
+    return out.transpose(1, 2).to(query.dtype)

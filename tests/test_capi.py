@@ -95,7 +95,8 @@ def _c_layout(struct_name, fields):
 
 @pytest.mark.parametrize("cls,name", [(_capi.FwdParams, "MimirPrefixLMFwdParams"),
                                       (_capi.BwdParams, "MimirPrefixLMBwdParams"),
-                                      (_capi.RopeParams, "MimirRopeParams")])
+                                      (_capi.RopeParams, "MimirRopeParams"),
+                                      (_capi.CacheAttnParams, "MimirCacheAttnParams")])
 def test_ctypes_struct_matches_c_layout(cls, name):
     fields = [f for f, _ in cls._fields_]
     size, offsets = _c_layout(name, fields)

@@ -117,3 +117,52 @@ def test_gated_attention_chain_fp64(with_rope):
     (dg_ref,) = torch.autograd.grad(y_ref, g, dy)
     assert torch.allclose(y, y_ref, rtol=1e-10, atol=1e-12)
     assert torch.allclose(dg.reshape(T, -1), dg_ref, rtol=1e-9, atol=1e-11)
+
+
+def test_cache_attention_empty_cache_is_prefixlm():
+    """cache_lengths = 0: causal == prefix-LM with p = 0, bidirectional == p = n (per batch row)."""
+    from oracle.prefixlm_oracle import dense_forward
+    torch.manual_seed(4)
+    B, S, hq, hkv, d, L = 3, 9, 4, 2, 16, 20
+    q = torch.randn(B, S, hq, d, dtype=torch.float64)
+    k = torch.randn(B, S, hkv, d, dtype=torch.float64)
+    v = torch.randn(B, S, hkv, d, dtype=torch.float64)
+    for causal in (True, False):
+        ck, cv = torch.zeros(B, L, hkv, d, dtype=torch.float64), torch.zeros(B, L, hkv, d, dtype=torch.float64)
+        out = LO.attention_with_cache(q, k, v, ck, cv, torch.zeros(B, dtype=torch.int64), causal)
+        cu = torch.arange(0, (B + 1) * S, S, dtype=torch.int32)
+        p = 0 if causal else S
+        pl = torch.full((B,), p, dtype=torch.int32)
+        cl = torch.full((B,), S - p, dtype=torch.int32)
+        ref = dense_forward(q.reshape(B * S, hq, d), k.reshape(B * S, hkv, d), v.reshape(B * S, hkv, d), False,
+                            pl, cl, cu, B * S, B)
+        assert torch.allclose(out.reshape(B * S, hq, d), ref, rtol=1e-10, atol=1e-12)
+        assert torch.equal(ck[:, :S], k) and torch.equal(cv[:, :S], v) and not ck[:, S:].any()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_cache_attention_brute_force(causal):
+    """Non-empty caches, chunked prefill and decode, GQA, batch_indices, against fp64 loops."""
+    torch.manual_seed(5)
+    B, hq, hkv, d, L = 3, 4, 2, 8, 24
+    for S in (1, 5):
+        q = torch.randn(B, S, hq, d, dtype=torch.float64)
+        k = torch.randn(B, S, hkv, d, dtype=torch.float64)
+        v = torch.randn(B, S, hkv, d, dtype=torch.float64)
+        ck, cv = torch.randn(5, L, hkv, d, dtype=torch.float64), torch.randn(5, L, hkv, d, dtype=torch.float64)
+        ck0, cv0 = ck.clone(), cv.clone()
+        lens = torch.tensor([0, 7, 13])
+        rows = torch.tensor([4, 0, 2])
+        out = LO.attention_with_cache(q, k, v, ck, cv, lens, causal, rows)
+        scale = d ** -0.5
+        for b in range(B):
+            r, c = int(rows[b]), int(lens[b])
+            keys, vals = ck0[r].clone(), cv0[r].clone()
+            keys[c:c + S], vals[c:c + S] = k[b], v[b]
+            assert torch.equal(ck[r, :c + S], keys[:c + S])
+            for i in range(S):
+                n = c + i + 1 if causal else c + S
+                for h in range(hq):
+                    kk, vv = keys[:n, h // (hq // hkv)], vals[:n, h // (hq // hkv)]
+                    w = torch.softmax((kk @ q[b, i, h]) * scale, dim=0)
+                    assert torch.allclose(out[b, i, h], w @ vv, rtol=1e-10, atol=1e-12)
