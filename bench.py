@@ -246,6 +246,83 @@ def layer_bench(torch, dev, args) -> int:
     return 0
 
 
+def cache_bench(torch, dev, args) -> int:
+    """KV-cache attention (src/mimir/model/layers.py:134-167) at the default workload's heads.
+
+    decode:  B = 8 rows, one new token each, cache lengths ~ U{1024..4096} (seed), L = 4096;
+             bound by reading the cache: bytes = sum_b kv_len_b * Hkv * D * 2 (K and V) * 2 B
+             plus q, out and the appended rows.
+    prefill: the same rows take a 512-token chunk on top of 1536 cached tokens (causal).
+    The reference composition (cache scatter, repeat_interleave, float mask, SDPA, and the
+    host read of kv_len.max()) runs on the same inputs for comparison.  One JSON line.
+    """
+    import torch.nn.functional as F
+    from mimir_amd.cache import Cache, attention_with_cache
+
+    B, hq, hkv, d, L = 8, 16, 4, 128, 4096
+    gen = torch.Generator().manual_seed(args.seed)
+    lens = torch.randint(1024, 4096 - 512, (B,), generator=gen)
+    ck = torch.randn(B, L, hkv, d, generator=gen).to(torch.bfloat16).to(dev)
+    cv = torch.randn(B, L, hkv, d, generator=gen).to(torch.bfloat16).to(dev)
+    cache = Cache(ck, cv)
+
+    def reference(q, k, v, cache_lengths, causal):
+        batch_size, seqlen = q.shape[:2]
+        positions = cache_lengths[:, None] + torch.arange(seqlen, device=dev, dtype=cache_lengths.dtype)
+        rows = torch.arange(batch_size, device=dev)
+        cache.keys[rows[:, None], positions] = k
+        cache.values[rows[:, None], positions] = v
+        kv_len = cache_lengths + seqlen
+        m = kv_len.max().item()
+        keys = cache.keys[:batch_size, :m].repeat_interleave(hq // hkv, dim=2)
+        values = cache.values[:batch_size, :m].repeat_interleave(hq // hkv, dim=2)
+        kp = torch.arange(m, device=dev)
+        valid = kp[None, :] < kv_len[:, None]
+        valid = valid[:, None, :] & (kp[None, None, :] <= positions[:, :, None]) if causal else valid[:, None, :]
+        mask = torch.zeros((batch_size, seqlen, m), dtype=q.dtype, device=dev).masked_fill(~valid, torch.finfo(q.dtype).min)
+        return F.scaled_dot_product_attention(q.transpose(1, 2), keys.transpose(1, 2), values.transpose(1, 2),
+                                              attn_mask=mask[:, None]).transpose(1, 2)
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    K, W = max(1, args.steps), max(1, args.warmup)
+    res = {"metric": "KV-cache decode attention GB/s (cache read)", "unit": "GB/s", "higher_is_better": True,
+           "steps": K, "warmup": W, "dtype": "bf16", "data": "synthetic",
+           "config": {"batch": B, "q_heads": hq, "kv_heads": hkv, "head_dim": d, "cache_len": L,
+                      "cache_lengths": lens.tolist(), "seed": args.seed}}
+    for name, S, causal in (("decode", 1, True), ("prefill", 512, True)):
+        cl = (lens if name == "decode" else torch.full((B,), 1536)).to(dev)
+        q = torch.randn(B, S, hq, d, generator=gen).to(torch.bfloat16).to(dev)
+        k = torch.randn(B, S, hkv, d, generator=gen).to(torch.bfloat16).to(dev)
+        v = torch.randn(B, S, hkv, d, generator=gen).to(torch.bfloat16).to(dev)
+        ms = timed(lambda: attention_with_cache(q, k, v, cache, cl, causal), K, W)
+        ms_ref = timed(lambda: reference(q, k, v, cl, causal), K, W)
+        kv = (cl.cpu() + S).tolist()
+        cache_bytes = sum(kv) * hkv * d * 2 * 2
+        io_bytes = 2 * B * S * hq * d * 2 + 2 * B * S * hkv * d * 2
+        pairs = sum(c * S + S * (S + 1) // 2 for c in cl.cpu().tolist())  # allowed (query, key) pairs
+        entry = {"ms": round(ms, 5), "reference_ms": round(ms_ref, 5), "speedup_vs_reference": round(ms_ref / ms, 2),
+                 "gbs": round((cache_bytes + io_bytes) / (ms * 1e-3) / 1e9, 1),
+                 "tflops": round(4 * d * hq * pairs / (ms * 1e-3) / 1e12, 2)}
+        entry["hbm_frac"] = round(entry["gbs"] / HBM_GBS, 4)
+        res[name] = entry
+    res["value"] = res["decode"]["gbs"]
+    res["roofline"] = {"kernel": "cache_attn_kernel<128> (+ combine)", "bound": "hbm", "achieved": res["decode"]["gbs"],
+                       "peak": HBM_GBS, "unit": "GB/s", "frac": res["decode"]["hbm_frac"]}
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +335,10 @@ def main() -> int:
                     help="instead of the operator, time the attention layer core (gqkv split, RoPE, attention, "
                          "sigmoid gate; fwd+bwd) fused (mimir_amd.layer) against the reference's composition of "
                          "torch ops around the same operator")
+    ap.add_argument("--cache", action="store_true",
+                    help="instead of the operator, time KV-cache attention (inference): decode (S = 1) and a "
+                         "prefill chunk into a filled cache, fused (mimir_amd.cache) against the reference's "
+                         "torch composition")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="instead of the step, time a plain device copy of this many MiB (reference kernel of known "
                          "HBM traffic for scaling the FETCH_SIZE / WRITE_SIZE counters)")
@@ -282,6 +363,8 @@ def main() -> int:
         return copy_calibration(torch, dev, args.copy_calibration_mib, max(1, args.steps))
     if args.layer:
         return layer_bench(torch, dev, args)
+    if args.cache:
+        return cache_bench(torch, dev, args)
     case = make_config(args.workload, seed=args.seed)
     c = case.to(dev)
     T, hq, d = c.q.shape

@@ -230,7 +230,9 @@ int mimir_prefixlm_rope(const MimirRopeParams* params, void* stream);
  *      softmax scale `softmax_scale`, out [b, i, h] in the element type.
  *
  * c + S must not exceed cache_len (the reference raises IndexError there; this
- * entry point skips the cache writes and keys beyond the cache instead).
+ * entry point skips the cache writes and keys beyond the cache instead), and a
+ * batch row whose cache row lies outside [0, cache_rows) gets a zero output and
+ * no cache write (the reference raises IndexError).
  * max_kv_len is an upper bound of max_b(c + S) (the reference's
  * kv_len.max().item(), layers.py:143) that sizes the key split.  bf16 only,
  * head_dim 64 or 128.  The workspace holds the split partial results. */
@@ -252,6 +254,7 @@ typedef struct MimirCacheAttnParams {
   int32_t batch;              /* B */
   int32_t seqlen;             /* S (1 for decode) */
   int32_t cache_len;          /* positions per cache row */
+  int32_t cache_rows;         /* rows of cache_k / cache_v; rows outside [0, cache_rows) are skipped */
   int32_t max_kv_len;         /* upper bound of max_b(cache_lengths[b] + S) */
   int32_t num_q_heads;
   int32_t num_kv_heads;

@@ -50,9 +50,13 @@ def attention_with_cache(query: Tensor, key: Tensor, value: Tensor, cache: Cache
     """``Attention._attention_with_cache`` (layers.py:134-167) for query [B, S, Hq, D] and
     key / value [B, S, Hkv, D]; updates ``cache`` in place and returns [B, S, Hq, D].
 
-    Like the reference (layers.py:143, ``kv_len.max().item()``) it reads the largest
-    cache length on the host once, and it raises ``IndexError`` where the reference's
-    cache write would index past the cache.
+    No host synchronisation by default: the key split is sized for the whole cache
+    (``cache_len`` positions) instead of the reference's ``kv_len.max().item()``
+    (layers.py:143), so decode steps can be captured in a HIP graph.  With
+    ``mimir_amd.set_validate_metadata(True)`` it reads the lengths once, as the
+    reference does, sizes the split exactly and raises ``IndexError`` where the
+    reference's cache write would index past the cache (without validation such
+    rows are not written and their keys are ignored).
     """
     if query.dtype != torch.bfloat16:
         raise TypeError(f"KV-cache attention supports bfloat16 tensors only, got {query.dtype}")
@@ -79,8 +83,8 @@ def attention_with_cache(query: Tensor, key: Tensor, value: Tensor, cache: Cache
         if rows.shape != (B,):
             raise ValueError(f"cache_batch_indices must be [{B}], got {tuple(rows.shape)}")
     L = ck.shape[1]
-    max_kv = 0
-    if B > 0:  # one host read for all checks (the reference reads kv_len.max() too)
+    max_kv = L
+    if B > 0 and P._validate_metadata:  # one host read for all checks (the reference reads kv_len.max() too)
         zero = torch.zeros((), dtype=torch.int32, device=device)
         lmax, lmin, rmin, rmax = torch.stack([lens.max(), lens.min(), rows.min() if rows is not None else zero,
                                               rows.max() if rows is not None else zero]).tolist()
@@ -100,7 +104,7 @@ def attention_with_cache(query: Tensor, key: Tensor, value: Tensor, cache: Cache
         q.data_ptr(), k.data_ptr(), v.data_ptr(), ck.data_ptr(), cv.data_ptr(), out.data_ptr(),
         lens.data_ptr(), rows.data_ptr() if rows is not None else None,
         *q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *ck.stride()[:3], *cv.stride()[:3], *out.stride()[:3],
-        B, S, L, max(max_kv, 1), hq, hkv, d, int(bool(causal)), _capi.DTYPE_BFLOAT16, scale, None, 0,
+        B, S, L, ck.shape[0], max(max_kv, 1), hq, hkv, d, int(bool(causal)), _capi.DTYPE_BFLOAT16, scale, None, 0,
     )
     ws_bytes = int(lib.mimir_prefixlm_cache_attn_workspace_bytes(ctypes.byref(p)))
     ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)

@@ -40,7 +40,7 @@ struct CacheArgs {
   const int32_t* batch_indices;
   int64_t q_sb, q_st, q_sh, kn_sb, kn_st, kn_sh, vn_sb, vn_st, vn_sh;
   int64_t ck_sb, ck_st, ck_sh, cv_sb, cv_st, cv_sh, o_sb, o_st, o_sh;
-  int B, S, L, Hkv, G, causal, D;
+  int B, S, L, rows, Hkv, G, causal, D;
   int n_rt;        // row tiles per (batch row, kv head)
   int splits;      // key splits per row tile
   int split_keys;  // keys per split, a multiple of kKeys
@@ -66,8 +66,8 @@ __global__ __launch_bounds__(256) void cache_append_kernel(const CacheArgs a) {
     const int i = (int)(t % a.S);
     const int b = (int)(t / a.S);
     const int pos = a.cache_lengths[b] + i;
-    if (pos < 0 || pos >= a.L) continue;  // beyond the cache: dropped
     const int64_t r = cache_row(a, b);
+    if (pos < 0 || pos >= a.L || r < 0 || r >= a.rows) continue;  // outside the cache: dropped
     *(bf16x8*)&a.ck[r * a.ck_sb + (int64_t)pos * a.ck_st + (int64_t)h * a.ck_sh + c * 8] =
         *(const bf16x8*)&a.kn[(int64_t)b * a.kn_sb + (int64_t)i * a.kn_st + (int64_t)h * a.kn_sh + c * 8];
     *(bf16x8*)&a.cv[r * a.cv_sb + (int64_t)pos * a.cv_st + (int64_t)h * a.cv_sh + c * 8] =
@@ -99,10 +99,12 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
   const int hk = u % a.Hkv;
   const int b = u / a.Hkv;
 
+  const int64_t crow = cache_row(a, b);
+  const bool row_in_cache = crow >= 0 && crow < a.rows;
   const int clen = clamp_len(a.cache_lengths[b], a.L);
-  const int kv = min(clen + a.S, a.L);  // keys of this batch row
+  const int kv = row_in_cache ? min(clen + a.S, a.L) : 0;  // keys of this batch row
   const int k0 = split * a.split_keys;
-  if (k0 >= kv) return;  // the combine reads only the splits that hold keys
+  if (k0 >= kv && (k0 > 0 || row_in_cache)) return;  // the combine reads only the splits that hold keys
   const int k1 = min(kv, k0 + a.split_keys);
   const int R = a.S * a.G;  // query rows (token-major (token, head) pairs)
 
@@ -124,9 +126,8 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
   const int kt0 = k0 / kKeys;
   const int kt1 = (min(k1, wg_kend) + kKeys - 1) / kKeys;  // may be <= kt0: nothing to attend
 
-  const int64_t crow = cache_row(a, b);
-  const bf16_t* kbase = a.ck + crow * a.ck_sb + (int64_t)hk * a.ck_sh;
-  const bf16_t* vbase = a.cv + crow * a.cv_sb + (int64_t)hk * a.cv_sh;
+  const bf16_t* kbase = a.ck + (row_in_cache ? crow : 0) * a.ck_sb + (int64_t)hk * a.ck_sh;
+  const bf16_t* vbase = a.cv + (row_in_cache ? crow : 0) * a.cv_sb + (int64_t)hk * a.cv_sh;
   const TileLoader<D, kWaves> ldk(a.ck_st, wave, lane), ldv(a.cv_st, wave, lane);
   if (kt0 < kt1) {
     ldk.issue(kbase, kt0 * kKeys, kv, sK0);
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
   const float l_tot = xor32_sum(l_run);
   if (a.splits == 1) {
     if (!row_ok) return;
-    const float inv = 1.f / l_tot;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;  // no keys (row outside the cache): zeros
     bf16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)ti * a.o_st + (int64_t)h * a.o_sh;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -274,46 +275,47 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
 }
 
 // out row = sum_c O_c * 2^(m_c - M) / sum_c l_c * 2^(m_c - M) over the splits
-// that hold keys of the batch row; 4 columns per thread.
+// that hold keys of the batch row.  One wave per output row: each lane owns D/64
+// columns and walks the splits (the (m, l) pair of a split is a broadcast load).
 __global__ __launch_bounds__(256) void cache_combine_kernel(const CacheArgs a) {
   const int R = a.S * a.G;
-  const int cols = a.D / 4;
-  const int64_t total = (int64_t)a.B * a.Hkv * R * cols;
-  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
-    const int c4 = (int)(idx % cols);
-    int64_t t = idx / cols;
-    const int row = (int)(t % R);
-    t /= R;
+  const int64_t rows_total = (int64_t)a.B * a.Hkv * R;
+  const int lane = threadIdx.x & 63;
+  const int cpl = a.D / 64;  // columns per lane (1 or 2)
+  for (int64_t wr = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 64; wr < rows_total;
+       wr += (int64_t)gridDim.x * 4) {
+    const int row = (int)(wr % R);
+    const int64_t t = wr / R;
     const int hk = (int)(t % a.Hkv);
     const int b = (int)(t / a.Hkv);
+    const int64_t crow = cache_row(a, b);
     const int clen = clamp_len(a.cache_lengths[b], a.L);
-    const int kv = min(clen + a.S, a.L);
+    const int kv = crow >= 0 && crow < a.rows ? min(clen + a.S, a.L) : 0;
     const int n_valid = min((kv + a.split_keys - 1) / a.split_keys, a.splits);
     const int rt = row / kRows, rr = row - rt * kRows;
     const int64_t unit0 = (((int64_t)b * a.Hkv + hk) * a.n_rt + rt) * a.splits;
     float M = -INFINITY;
+#pragma unroll 4
     for (int c = 0; c < n_valid; ++c) M = fmaxf(M, a.part_ml[2 * ((unit0 + c) * kRows + rr)]);
-    float lsum = 0.f;
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f, o0 = 0.f, o1 = 0.f;
     if (M != -INFINITY) {
+#pragma unroll 4
       for (int c = 0; c < n_valid; ++c) {
         const int64_t slot = (unit0 + c) * kRows + rr;
         const float m = a.part_ml[2 * slot];
-        if (m == -INFINITY) continue;
-        const float w = fast_exp2(m - M);
+        const float w = m == -INFINITY ? 0.f : fast_exp2(m - M);
         lsum += a.part_ml[2 * slot + 1] * w;
-        const f32x4 pv = *(const f32x4*)&a.part_o[slot * a.D + 4 * c4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] += pv[e] * w;
+        const float* po = a.part_o + slot * a.D + lane * cpl;
+        o0 += po[0] * w;
+        if (cpl > 1) o1 += po[1] * w;
       }
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     const int ti = row / a.G;
     const int h = hk * a.G + (row - ti * a.G);
-    bf16x4 ob;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) ob[e] = (bf16_t)(o[e] * inv);
-    *(bf16x4*)&a.out[(int64_t)b * a.o_sb + (int64_t)ti * a.o_st + (int64_t)h * a.o_sh + 4 * c4] = ob;
+    bf16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)ti * a.o_st + (int64_t)h * a.o_sh + lane * cpl;
+    orow[0] = (bf16_t)(o0 * inv);
+    if (cpl > 1) orow[1] = (bf16_t)(o1 * inv);
   }
 }
 
@@ -333,7 +335,7 @@ CacheSplit cache_split(const MimirCacheAttnParams& p) {
   if (max_kv < 1) max_kv = 1;
   const int tiles = (max_kv + kKeys - 1) / kKeys;
   const int64_t base = (int64_t)p.batch * p.num_kv_heads * s.n_rt;
-  const int64_t target = 4 * (int64_t)device_cu_count();  // workgroups to cover the chip
+  const int64_t target = 2 * (int64_t)device_cu_count();  // workgroups to cover the chip (two per CU)
   int64_t splits = base > 0 ? (target + base - 1) / base : 1;
   if (splits < 1) splits = 1;
   if (splits > tiles) splits = tiles;
@@ -365,6 +367,7 @@ hipError_t launch_cache_attn_bf16(const MimirCacheAttnParams& p, hipStream_t str
   a.B = p.batch;
   a.S = p.seqlen;
   a.L = p.cache_len;
+  a.rows = p.cache_rows;
   a.Hkv = p.num_kv_heads;
   a.G = p.num_q_heads / p.num_kv_heads;
   a.causal = p.causal != 0;
@@ -385,8 +388,8 @@ hipError_t launch_cache_attn_bf16(const MimirCacheAttnParams& p, hipStream_t str
   else
     hipLaunchKernelGGL(cache_attn_kernel<64>, dim3((unsigned)sp.units), dim3(kThreads), 0, stream, a);
   if ((e = hipGetLastError()) != hipSuccess || sp.splits == 1) return e;
-  const int64_t combines = (int64_t)a.B * a.Hkv * a.S * a.G * (a.D / 4);
-  hipLaunchKernelGGL(cache_combine_kernel, dim3(grid_for(combines)), dim3(256), 0, stream, a);
+  const int64_t combine_threads = (int64_t)a.B * a.Hkv * a.S * a.G * 64;  // one wave per row
+  hipLaunchKernelGGL(cache_combine_kernel, dim3(grid_for(combine_threads)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -266,7 +266,8 @@ int mimir_prefixlm_cache_attn(const MimirCacheAttnParams* p, void* stream) {
   if (p->dtype != MIMIR_DTYPE_BFLOAT16)
     return fail(MIMIR_ERR_UNSUPPORTED_DTYPE, "KV-cache attention supports bfloat16 tensors only (dtype code " +
                                                  std::to_string(p->dtype) + ")");
-  if (p->batch < 0 || p->seqlen < 0 || p->cache_len < 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0)
+  if (p->batch < 0 || p->seqlen < 0 || p->cache_len < 0 || p->cache_rows < 0 || p->num_q_heads <= 0 ||
+      p->num_kv_heads <= 0)
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "negative size or non-positive head count");
   if (p->num_q_heads % p->num_kv_heads != 0)
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "Query heads " + std::to_string(p->num_q_heads) +

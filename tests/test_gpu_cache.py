@@ -63,9 +63,36 @@ def test_unsplit_launch(device):
     _run(device, B=4, S=1024, hq=16, hkv=4, d=128, L=1100, lens=[0, 3, 40, 76], causal=True, seed=3)
 
 
-def test_write_past_the_cache_raises(device):
-    q = torch.zeros(1, 4, 2, 64, dtype=BF16, device=device)
-    k = torch.zeros(1, 4, 2, 64, dtype=BF16, device=device)
-    cache = Cache.create(1, 10, 2, 64, dtype=BF16, device=device)
-    with pytest.raises(IndexError):
-        attention_with_cache(q, k, k, cache, torch.tensor([7], device=device), True)
+@pytest.mark.parametrize("validate", [True, False])
+def test_validated_lengths(device, validate):
+    """With validation the split is sized from the actual lengths; a write past the cache raises."""
+    from mimir_amd import set_validate_metadata
+    set_validate_metadata(validate)
+    try:
+        _run(device, B=3, S=1, hq=4, hkv=1, d=128, L=3000, lens=[10, 2000, 700], causal=True, seed=4)
+        if validate:
+            q = torch.zeros(1, 4, 2, 64, dtype=BF16, device=device)
+            k = torch.zeros(1, 4, 2, 64, dtype=BF16, device=device)
+            cache = Cache.create(1, 10, 2, 64, dtype=BF16, device=device)
+            with pytest.raises(IndexError):
+                attention_with_cache(q, k, k, cache, torch.tensor([7], device=device), True)
+    finally:
+        set_validate_metadata(False)
+
+
+def test_rows_outside_the_cache_are_skipped(device):
+    """Without validation a batch index outside the cache writes nothing and yields zeros."""
+    gen = torch.Generator().manual_seed(9)
+    q = torch.randn(2, 1, 4, 128, generator=gen).to(BF16).to(device)
+    k = torch.randn(2, 1, 2, 128, generator=gen).to(BF16).to(device)
+    cache = Cache(torch.randn(2, 64, 2, 128, generator=gen).to(BF16).to(device),
+                  torch.randn(2, 64, 2, 128, generator=gen).to(BF16).to(device))
+    before = cache.keys.clone()
+    out = attention_with_cache(q, k, k, cache, torch.tensor([3, 5], device=device), True,
+                               torch.tensor([1, 7], device=device))
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[1]) == 0 and torch.isfinite(out).all()
+    assert torch.equal(cache.keys[0], before[0])
+    # batch row 0 -> cache row 1, position cache_lengths[0] = 3
+    assert torch.equal(cache.keys[1, 3], k[0, 0]) and torch.equal(cache.keys[1, :3], before[1, :3])
+    assert torch.equal(cache.keys[1, 4:], before[1, 4:])
