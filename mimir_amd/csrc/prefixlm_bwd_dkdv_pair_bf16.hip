@@ -166,15 +166,63 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   auto compute = [&](bool masked, int qr, const bf16_t* sQ, const bf16_t* sdO, const float* sL,
                      const float* sD) {  // qr = first query row of this wave's half
     f32x16 sc = f32x16{}, dp = f32x16{};
+    // Per-step copies of the lane offsets: recomputing the stage addresses from
+    // them each step keeps one register per offset live instead of one per
+    // (stage, operand) pair, which leaves the registers for reading operands ahead.
+    int opb = tl.op_base + qh * 32 * L::kRowElems, trb = tl.tr_base + qh * 32 * L::kRowElems,
+        lrow = 32 * qh + 4 * hi;
+    __asm__ volatile("" : "+v"(opb), "+v"(trb), "+v"(lrow));
+    // The LDS operand reads run two MFMA pairs ahead of their use; the
+    // scheduling barriers keep the compiler from pulling them back next to the
+    // MFMAs (which would leave every MFMA waiting for its own read).
+    bf16x8 qa[KS], oa[KS], va[KS];
+    auto rd_a = [&](int ks) {
+      qa[ks] = *(const bf16x8*)&sQ[opb + ks * 16];
+      oa[ks] = *(const bf16x8*)&sdO[opb + ks * 16];
+      va[ks] = *(const bf16x8*)&sVs[ks * 16];
+    };
+    // dV / dK operand pair j (16-query step j / 4 of this wave's half, 32 columns j % 4)
+    bf16x8 ot[3], qt[3];
+    auto rd_tr = [&](int j) {
+      const int o = trb + (j >> 2) * 16 * L::kRowElems + (j & 3) * 32;
+      ot[j % 3] = cat8(lds_read_tr16(&sdO[o]), lds_read_tr16(&sdO[o + L::kTrSecond]));
+      qt[j % 3] = cat8(lds_read_tr16(&sQ[o]), lds_read_tr16(&sQ[o + L::kTrSecond]));
+    };
+    f32x4 l4[2], d4[2];  // lse2 / delta of the rows of one 16-query step
+    auto rd_ld = [&](int s2) {
+#pragma unroll
+      for (int rg2 = 0; rg2 < 2; ++rg2) {
+        l4[rg2] = *(const f32x4*)&sL[lrow + 8 * (2 * s2 + rg2)];
+        d4[rg2] = *(const f32x4*)&sD[lrow + 8 * (2 * s2 + rg2)];
+      }
+    };
+    f32x8 tp, tds;
+    auto softmax = [&](int s2, int rg2) {  // P and dS of rows 8 (2 s2 + rg2) + 4 hi + e
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * (2 * s2 + rg2) + e;
+        const float pr = fast_exp2(__builtin_fmaf(sc[r], c2, -l4[rg2][e]));
+        tp[4 * rg2 + e] = pr;
+        tds[4 * rg2 + e] = pr * (dp[r] - d4[rg2][e]);
+      }
+    };
+
     // S / dP MFMAs at raised wave priority: of the two waves on a SIMD, the one
     // ready to issue MFMAs goes first while the other runs its softmax.
     __builtin_amdgcn_s_setprio(1);
+    rd_a(0);
+    rd_a(1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const int o = tl.op_base + qh * 32 * L::kRowElems + ks * 16;
-      sc = mfma32(*(const bf16x8*)&sQ[o], kf[ks], sc);
-      dp = mfma32(*(const bf16x8*)&sdO[o], *(const bf16x8*)&sVs[ks * 16], dp);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 2 < KS) rd_a(ks + 2);
+      sc = mfma32(qa[ks], kf[ks], sc);
+      dp = mfma32(oa[ks], va[ks], dp);
     }
+    rd_ld(0);
+    rd_tr(0);
+    rd_tr(1);
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(0);
     // rows of sc / dp: query qr + 8*(r/4) + 4*hi + r%4 ; column: the lane's key.
     if (masked) {
@@ -187,33 +235,26 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
       for (int r = 0; r < 16; ++r)
         if (base + (unsigned)(8 * (r >> 2) + (r & 3)) >= lim) sc[r] = -INFINITY;
     }
+    bf16x8 pb[2], db[2];
+    softmax(0, 0);
+    softmax(0, 1);
+    pb[0] = to_bf16x8(tp);
+    db[0] = to_bf16x8(tds);
+    rd_ld(1);
+    // Eight dV / dK MFMA pairs; the softmax of the second 16-query step runs
+    // beside the first four.
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      f32x8 tp, tds;
-#pragma unroll
-      for (int rg2 = 0; rg2 < 2; ++rg2) {
-        const int rg = 2 * s2 + rg2;
-        const int qr0 = 32 * qh + 8 * rg + 4 * hi;
-        const f32x4 l4 = *(const f32x4*)&sL[qr0];
-        const f32x4 d4 = *(const f32x4*)&sD[qr0];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * rg + e;
-          const float pr = fast_exp2(__builtin_fmaf(sc[r], c2, -l4[e]));
-          tp[4 * rg2 + e] = pr;
-          tds[4 * rg2 + e] = pr * (dp[r] - d4[e]);
-        }
-      }
-      const bf16x8 pb = to_bf16x8(tp);
-      const bf16x8 db = to_bf16x8(tds);
-      const int kk = 2 * qh + s2;  // 16-query step inside the 64-row tile
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int o = tl.tr_base + kk * 16 * L::kRowElems + dt * 32;
-        const bf16x8 ot = cat8(lds_read_tr16(&sdO[o]), lds_read_tr16(&sdO[o + L::kTrSecond]));
-        const bf16x8 qt = cat8(lds_read_tr16(&sQ[o]), lds_read_tr16(&sQ[o + L::kTrSecond]));
-        dvacc[dt] = mfma32(ot, pb, dvacc[dt]);
-        dkacc[dt] = mfma32(qt, db, dkacc[dt]);
+    for (int j = 0; j < 8; ++j) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + 2 < 8) rd_tr(j + 2);
+      const int dt = j & 3, s2 = j >> 2;
+      dvacc[dt] = mfma32(ot[j % 3], pb[s2], dvacc[dt]);
+      dkacc[dt] = mfma32(qt[j % 3], db[s2], dkacc[dt]);
+      if (j == 1) softmax(1, 0);
+      if (j == 2) softmax(1, 1);
+      if (j == 3) {
+        pb[1] = to_bf16x8(tp);
+        db[1] = to_bf16x8(tds);
       }
     }
   };
