@@ -234,8 +234,11 @@ int mimir_prefixlm_rope(const MimirRopeParams* params, void* stream);
  * batch row whose cache row lies outside [0, cache_rows) gets a zero output and
  * no cache write (the reference raises IndexError).
  * max_kv_len is an upper bound of max_b(c + S) (the reference's
- * kv_len.max().item(), layers.py:143) that sizes the key split.  bf16 only,
- * head_dim 64 or 128.  The workspace holds the split partial results. */
+ * kv_len.max().item(), layers.py:143) that sizes the key split; each batch
+ * row's own key range is split evenly over it.  bf16 only, head_dim 64 or 128.
+ * The workspace holds the split partial results and one arrival counter per
+ * (batch row, kv head, 128-row tile), which the call clears itself (no memset:
+ * the call can be captured in a graph). */
 typedef struct MimirCacheAttnParams {
   const void* q;              /* [B, S, Hq, D] */
   const void* k_new;          /* [B, S, Hkv, D] */
@@ -243,8 +246,8 @@ typedef struct MimirCacheAttnParams {
   void* cache_k;              /* [>= rows, cache_len, Hkv, D] */
   void* cache_v;              /* [>= rows, cache_len, Hkv, D] */
   void* out;                  /* [B, S, Hq, D] */
-  const int32_t* cache_lengths;   /* device int32 [B] */
-  const int32_t* batch_indices;   /* device int32 [B] or NULL (row b) */
+  const void* cache_lengths;   /* device int32 or int64 [B] (index_int64) */
+  const void* batch_indices;   /* device int32 or int64 [B], or NULL (row b) */
   int64_t q_stride_batch, q_stride_token, q_stride_head;
   int64_t kn_stride_batch, kn_stride_token, kn_stride_head;
   int64_t vn_stride_batch, vn_stride_token, vn_stride_head;
@@ -264,6 +267,7 @@ typedef struct MimirCacheAttnParams {
   float softmax_scale;
   void* workspace;            /* >= mimir_prefixlm_cache_attn_workspace_bytes(params) */
   size_t workspace_bytes;
+  int32_t index_int64;        /* 1: cache_lengths / batch_indices are int64, 0: int32 */
 } MimirCacheAttnParams;
 size_t mimir_prefixlm_cache_attn_workspace_bytes(const MimirCacheAttnParams* params);
 int mimir_prefixlm_cache_attn(const MimirCacheAttnParams* params, void* stream);

@@ -96,6 +96,7 @@ class CacheAttnParams(ctypes.Structure):
         ("batch", _i32), ("seqlen", _i32), ("cache_len", _i32), ("cache_rows", _i32), ("max_kv_len", _i32),
         ("num_q_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32), ("causal", _i32), ("dtype", _i32),
         ("softmax_scale", ctypes.c_float), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("index_int64", _i32),
     ]
 
 

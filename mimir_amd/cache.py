@@ -74,18 +74,20 @@ def attention_with_cache(query: Tensor, key: Tensor, value: Tensor, cache: Cache
         raise ValueError("cache tensors need a unit head_dim stride")
     q, k, v = _rows4("query", query), _rows4("key", key), _rows4("value", value)
     device = q.device
-    lens = cache_lengths.to(device=device, dtype=torch.int32).contiguous()
+    # int32 and int64 indices are read as they are (no conversion launch)
+    index_dtype = cache_lengths.dtype if cache_lengths.dtype in (torch.int32, torch.int64) else torch.int64
+    lens = cache_lengths.to(device=device, dtype=index_dtype).contiguous()
     if lens.shape != (B,):
         raise ValueError(f"cache_lengths must be [{B}], got {tuple(lens.shape)}")
     rows = None
     if cache_batch_indices is not None:
-        rows = cache_batch_indices.to(device=device, dtype=torch.int32).contiguous()
+        rows = cache_batch_indices.to(device=device, dtype=index_dtype).contiguous()
         if rows.shape != (B,):
             raise ValueError(f"cache_batch_indices must be [{B}], got {tuple(rows.shape)}")
     L = ck.shape[1]
     max_kv = L
     if B > 0 and P._validate_metadata:  # one host read for all checks (the reference reads kv_len.max() too)
-        zero = torch.zeros((), dtype=torch.int32, device=device)
+        zero = torch.zeros((), dtype=index_dtype, device=device)
         lmax, lmin, rmin, rmax = torch.stack([lens.max(), lens.min(), rows.min() if rows is not None else zero,
                                               rows.max() if rows is not None else zero]).tolist()
         max_kv = lmax + S
@@ -105,6 +107,7 @@ def attention_with_cache(query: Tensor, key: Tensor, value: Tensor, cache: Cache
         lens.data_ptr(), rows.data_ptr() if rows is not None else None,
         *q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *ck.stride()[:3], *cv.stride()[:3], *out.stride()[:3],
         B, S, L, ck.shape[0], max(max_kv, 1), hq, hkv, d, int(bool(causal)), _capi.DTYPE_BFLOAT16, scale, None, 0,
+        int(index_dtype == torch.int64),
     )
     ws_bytes = int(lib.mimir_prefixlm_cache_attn_workspace_bytes(ctypes.byref(p)))
     ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)

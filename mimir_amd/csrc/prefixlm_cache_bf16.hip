@@ -6,19 +6,21 @@
 // (and j <= cache_lengths[b] + i when causal).  The reference materializes the
 // repeated K/V heads and a [B, S, max_kv_len] mask for SDPA; here:
 //
-//   cache_append_kernel   the scatter of k_new / v_new into the cache rows
+//   cache_append_kernel   the scatter of k_new / v_new into the cache rows (it
+//                         also clears the split arrival counters)
 //   cache_attn_kernel     one workgroup per (batch row, kv head, 128 query rows,
 //                         key split): the G query heads of a kv head share its
 //                         K / V tiles (rows are (token, head) pairs, token-major),
 //                         64-key tiles stream through two LDS stages, S^T = K Q^T
 //                         and O^T += V^T P^T on bf16 MFMA with an online softmax
-//                         (the forward kernel's arithmetic)
-//   cache_combine_kernel  merges the key splits' partial (max, sum, O) rows
+//                         (the forward kernel's arithmetic).  With several
+//                         splits, each publishes its partial (max, sum, O) rows
+//                         and the last to arrive merges them into the output.
 //
-// Decode (S = 1) has only G rows per kv head, so the key range is split over
-// enough workgroups to cover the chip (flash-decoding); the kernel is then
-// bound by the HBM read of the cache.  Prefill with a long S fills the row
-// tiles and runs on the MFMA like the forward kernel.
+// Decode (S = 1) has only G rows per kv head, so each batch row's key range is
+// split evenly over enough workgroups to cover the chip (flash-decoding); the
+// kernel is then bound by the HBM read of the cache.  Prefill with a long S
+// fills the row tiles and runs on the MFMA like the forward kernel.
 #include "prefixlm_common.h"
 
 namespace mimir {
@@ -36,26 +38,36 @@ struct CacheArgs {
   bf16_t* ck;
   bf16_t* cv;
   bf16_t* out;
-  const int32_t* cache_lengths;
-  const int32_t* batch_indices;
+  const void* cache_lengths;  // int32 or int64 (idx64)
+  const void* batch_indices;  // int32 or int64, or null
+  int idx64;
   int64_t q_sb, q_st, q_sh, kn_sb, kn_st, kn_sh, vn_sb, vn_st, vn_sh;
   int64_t ck_sb, ck_st, ck_sh, cv_sb, cv_st, cv_sh, o_sb, o_st, o_sh;
   int B, S, L, rows, Hkv, G, causal, D;
   int n_rt;        // row tiles per (batch row, kv head)
-  int splits;      // key splits per row tile
-  int split_keys;  // keys per split, a multiple of kKeys
+  int splits;      // key splits per row tile (each batch row's key tiles spread evenly over them)
   float scale_log2;
   float* part_o;   // [unit, kRows, D] unnormalized O of each split (splits > 1)
   float* part_ml;  // [unit, kRows, 2]: running max (exp2 domain) and sum
+  int* counters;   // [B * Hkv * n_rt] split arrivals per row tile (splits > 1), cleared by the append kernel
+  int n_counters;
 };
 
-__device__ __forceinline__ int cache_row(const CacheArgs& a, int b) {
-  return a.batch_indices != nullptr ? a.batch_indices[b] : b;
+__device__ __forceinline__ int64_t load_index(const void* p, int i, int idx64) {
+  return idx64 ? ((const int64_t*)p)[i] : (int64_t)((const int32_t*)p)[i];
 }
-__device__ __forceinline__ int clamp_len(int c, int L) { return c < 0 ? 0 : (c > L ? L : c); }
+__device__ __forceinline__ int64_t cache_row(const CacheArgs& a, int b) {
+  return a.batch_indices != nullptr ? load_index(a.batch_indices, b, a.idx64) : b;
+}
+// cache_lengths[b] clamped to [0, L]
+__device__ __forceinline__ int cache_len_of(const CacheArgs& a, int b) {
+  const int64_t c = load_index(a.cache_lengths, b, a.idx64);
+  return c < 0 ? 0 : (c > a.L ? a.L : (int)c);
+}
 
 // k_new / v_new [b, i, h] -> cache [row(b), cache_lengths[b] + i, h]; 16 bytes per thread.
 __global__ __launch_bounds__(256) void cache_append_kernel(const CacheArgs a) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < a.n_counters; i += gridDim.x * 256) a.counters[i] = 0;
   const int chunks = a.D / 8;
   const int64_t total = (int64_t)a.B * a.S * a.Hkv * chunks;
   for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
@@ -65,7 +77,7 @@ __global__ __launch_bounds__(256) void cache_append_kernel(const CacheArgs a) {
     t /= a.Hkv;
     const int i = (int)(t % a.S);
     const int b = (int)(t / a.S);
-    const int pos = a.cache_lengths[b] + i;
+    const int64_t pos = load_index(a.cache_lengths, b, a.idx64) + i;
     const int64_t r = cache_row(a, b);
     if (pos < 0 || pos >= a.L || r < 0 || r >= a.rows) continue;  // outside the cache: dropped
     *(bf16x8*)&a.ck[r * a.ck_sb + (int64_t)pos * a.ck_st + (int64_t)h * a.ck_sh + c * 8] =
@@ -101,11 +113,16 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
 
   const int64_t crow = cache_row(a, b);
   const bool row_in_cache = crow >= 0 && crow < a.rows;
-  const int clen = clamp_len(a.cache_lengths[b], a.L);
+  const int clen = cache_len_of(a, b);
   const int kv = row_in_cache ? min(clen + a.S, a.L) : 0;  // keys of this batch row
-  const int k0 = split * a.split_keys;
-  if (k0 >= kv && (k0 > 0 || row_in_cache)) return;  // the combine reads only the splits that hold keys
-  const int k1 = min(kv, k0 + a.split_keys);
+  // This batch row's key tiles, spread evenly over the splits; n_valid splits
+  // hold keys.  A row without keys (outside the cache) gets zeros from split 0.
+  const int tiles_b = (kv + kKeys - 1) / kKeys;
+  const int per = max(1, (tiles_b + a.splits - 1) / a.splits);
+  const int n_valid = (tiles_b + per - 1) / per;
+  if (split > 0 && split >= n_valid) return;
+  const int k0 = split * per * kKeys;
+  const int k1 = min(kv, k0 + per * kKeys);
   const int R = a.S * a.G;  // query rows (token-major (token, head) pairs)
 
   // This lane's row and its key limit.
@@ -238,10 +255,9 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
     compute(kt + 1, sK1, sV1);
   }
 
-  if (!wave_active) return;
   const float l_tot = xor32_sum(l_run);
-  if (a.splits == 1) {
-    if (!row_ok) return;
+  if (n_valid <= 1) {
+    if (!wave_active || !row_ok) return;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;  // no keys (row outside the cache): zeros
     bf16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)ti * a.o_st + (int64_t)h * a.o_sh;
 #pragma unroll
@@ -255,65 +271,79 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
       }
     return;
   }
-  // Partial result of this split: unnormalized O, the max in the exp2 domain
-  // (-inf: no key of this split is allowed for the row) and the sum.
-  const int64_t slot = (int64_t)blockIdx.x * kRows + wave * 32 + l32;
-  float* po = a.part_o + slot * D;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      f32x4 t;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) t[e] = oacc[dt][4 * rg + e];
-      *(f32x4*)&po[32 * dt + 8 * rg + 4 * hi] = t;
-    }
-  if (hi == 0) {
-    a.part_ml[2 * slot] = m_run == -INFINITY ? -INFINITY : m_run * c2;
-    a.part_ml[2 * slot + 1] = l_tot;
-  }
-}
 
-// out row = sum_c O_c * 2^(m_c - M) / sum_c l_c * 2^(m_c - M) over the splits
-// that hold keys of the batch row.  One wave per output row: each lane owns D/64
-// columns and walks the splits (the (m, l) pair of a split is a broadcast load).
-__global__ __launch_bounds__(256) void cache_combine_kernel(const CacheArgs a) {
-  const int R = a.S * a.G;
-  const int64_t rows_total = (int64_t)a.B * a.Hkv * R;
-  const int lane = threadIdx.x & 63;
-  const int cpl = a.D / 64;  // columns per lane (1 or 2)
-  for (int64_t wr = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 64; wr < rows_total;
-       wr += (int64_t)gridDim.x * 4) {
-    const int row = (int)(wr % R);
-    const int64_t t = wr / R;
-    const int hk = (int)(t % a.Hkv);
-    const int b = (int)(t / a.Hkv);
-    const int64_t crow = cache_row(a, b);
-    const int clen = clamp_len(a.cache_lengths[b], a.L);
-    const int kv = crow >= 0 && crow < a.rows ? min(clen + a.S, a.L) : 0;
-    const int n_valid = min((kv + a.split_keys - 1) / a.split_keys, a.splits);
-    const int rt = row / kRows, rr = row - rt * kRows;
-    const int64_t unit0 = (((int64_t)b * a.Hkv + hk) * a.n_rt + rt) * a.splits;
+  // Several splits hold keys of this row tile: publish this split's partial
+  // rows -- unnormalized O, the max in the exp2 domain (-inf: no allowed key)
+  // and the sum -- with device-coherent stores; the last split to arrive (per
+  // row tile) reads them all back the same way and writes the merged rows.
+  // The stores are complete before the arrival count, and the loads are issued
+  // after it has returned, so no cache flush is needed.
+  constexpr int kDevScope = 16;  // buffer cache policy: coherent at device scope
+  const int64_t units = (int64_t)gridDim.x;
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(a.part_o, (uint32_t)(units * kRows * D * 4));
+  const __amdgpu_buffer_rsrc_t rml = make_rsrc(a.part_ml, (uint32_t)(units * kRows * 2 * 4));
+  const int rt_rows = min(kRows, R - rt * kRows);
+  if (wave_active) {
+    const uint32_t slot = (uint32_t)blockIdx.x * kRows + wave * 32 + l32;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        f32x4 t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = oacc[dt][4 * rg + e];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, t), ro,
+                                               (slot * D + 32 * dt + 8 * rg + 4 * hi) * 4, 0, kDevScope);
+      }
+    if (hi == 0) {
+      const float m2 = m_run == -INFINITY ? -INFINITY : m_run * c2;
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, f32x2{m2, l_tot}), rml, slot * 8, 0,
+                                            kDevScope);
+    }
+  }
+  __asm__ volatile("" ::: "memory");
+  wait_vmem();  // the partial rows are stored
+  __shared__ int last;
+  __syncthreads();
+  const int group = blockIdx.x / a.splits;  // (batch row, kv head, row tile)
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(&a.counters[group], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_valid - 1;
+  __syncthreads();
+  if (!last) return;
+  // out row = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M) over the n_valid
+  // splits; one wave per row, each lane D / 64 columns.
+  const uint32_t unit0 = (uint32_t)group * a.splits;
+  const int cpl = D / 64;
+  for (int rr = wave; rr < rt_rows; rr += kWaves) {
     float M = -INFINITY;
-#pragma unroll 4
-    for (int c = 0; c < n_valid; ++c) M = fmaxf(M, a.part_ml[2 * ((unit0 + c) * kRows + rr)]);
+    for (int c = 0; c < n_valid; ++c) {
+      const f32x2 ml = __builtin_bit_cast(
+          f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, ((unit0 + c) * kRows + rr) * 8, 0, kDevScope));
+      M = fmaxf(M, ml[0]);
+    }
     float lsum = 0.f, o0 = 0.f, o1 = 0.f;
     if (M != -INFINITY) {
-#pragma unroll 4
       for (int c = 0; c < n_valid; ++c) {
-        const int64_t slot = (unit0 + c) * kRows + rr;
-        const float m = a.part_ml[2 * slot];
-        const float w = m == -INFINITY ? 0.f : fast_exp2(m - M);
-        lsum += a.part_ml[2 * slot + 1] * w;
-        const float* po = a.part_o + slot * a.D + lane * cpl;
-        o0 += po[0] * w;
-        if (cpl > 1) o1 += po[1] * w;
+        const uint32_t slot = (unit0 + c) * kRows + rr;
+        const f32x2 ml = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, slot * 8, 0, kDevScope));
+        const float w = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - M);
+        lsum += ml[1] * w;
+        if (cpl > 1) {
+          const f32x2 o = __builtin_bit_cast(
+              f32x2, __builtin_amdgcn_raw_buffer_load_b64(ro, (slot * D + lane * 2) * 4, 0, kDevScope));
+          o0 += o[0] * w;
+          o1 += o[1] * w;
+        } else {
+          o0 += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, (slot * D + lane) * 4, 0,
+                                                                               kDevScope)) * w;
+        }
       }
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    const int ti = row / a.G;
-    const int h = hk * a.G + (row - ti * a.G);
-    bf16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)ti * a.o_st + (int64_t)h * a.o_sh + lane * cpl;
+    const int row_g = rt * kRows + rr;
+    const int ti_r = row_g / a.G;
+    const int h_r = hk * a.G + (row_g - ti_r * a.G);
+    bf16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)ti_r * a.o_st + (int64_t)h_r * a.o_sh + lane * cpl;
     orow[0] = (bf16_t)(o0 * inv);
     if (cpl > 1) orow[1] = (bf16_t)(o1 * inv);
   }
@@ -334,16 +364,16 @@ CacheSplit cache_split(const MimirCacheAttnParams& p) {
   int max_kv = p.max_kv_len < p.cache_len ? p.max_kv_len : p.cache_len;
   if (max_kv < 1) max_kv = 1;
   const int tiles = (max_kv + kKeys - 1) / kKeys;
-  const int64_t base = (int64_t)p.batch * p.num_kv_heads * s.n_rt;
+  s.groups = (int64_t)p.batch * p.num_kv_heads * s.n_rt;
   const int64_t target = 2 * (int64_t)device_cu_count();  // workgroups to cover the chip (two per CU)
-  int64_t splits = base > 0 ? (target + base - 1) / base : 1;
+  int64_t splits = s.groups > 0 ? (target + s.groups - 1) / s.groups : 1;
   if (splits < 1) splits = 1;
   if (splits > tiles) splits = tiles;
-  const int tiles_per_split = (int)((tiles + splits - 1) / splits);
-  s.split_keys = tiles_per_split * kKeys;
-  s.splits = (max_kv + s.split_keys - 1) / s.split_keys;
-  s.units = base * s.splits;
-  s.workspace_bytes = s.splits > 1 ? (size_t)s.units * kRows * ((size_t)p.head_dim + 2) * sizeof(float) : 0;
+  s.splits = (int)splits;
+  s.units = s.groups * s.splits;
+  // partial O, then (max, sum) per unit row, then the arrival counters
+  s.workspace_bytes =
+      s.splits > 1 ? (size_t)s.units * kRows * ((size_t)p.head_dim + 2) * sizeof(float) + (size_t)s.groups * 4 : 0;
   return s;
 }
 
@@ -372,14 +402,17 @@ hipError_t launch_cache_attn_bf16(const MimirCacheAttnParams& p, hipStream_t str
   a.G = p.num_q_heads / p.num_kv_heads;
   a.causal = p.causal != 0;
   a.D = p.head_dim;
+  a.idx64 = p.index_int64 != 0;
   a.n_rt = sp.n_rt;
   a.splits = sp.splits;
-  a.split_keys = sp.split_keys;
   a.scale_log2 = p.softmax_scale * kLog2e;
   a.part_o = (float*)p.workspace;
   a.part_ml = a.part_o + (size_t)sp.units * kRows * p.head_dim;
+  a.counters = (int*)(a.part_ml + (size_t)sp.units * kRows * 2);
+  a.n_counters = sp.splits > 1 ? (int)sp.groups : 0;
   if (sp.splits > 1 && p.workspace == nullptr) return hipErrorInvalidValue;
   const int64_t appends = (int64_t)a.B * a.S * a.Hkv * (a.D / 8);
+  // units > 0 implies appends > 0, so the counters are always cleared before use
   if (appends > 0) hipLaunchKernelGGL(cache_append_kernel, dim3(grid_for(appends)), dim3(256), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || sp.units == 0) return e;
@@ -387,9 +420,6 @@ hipError_t launch_cache_attn_bf16(const MimirCacheAttnParams& p, hipStream_t str
     hipLaunchKernelGGL(cache_attn_kernel<128>, dim3((unsigned)sp.units), dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(cache_attn_kernel<64>, dim3((unsigned)sp.units), dim3(kThreads), 0, stream, a);
-  if ((e = hipGetLastError()) != hipSuccess || sp.splits == 1) return e;
-  const int64_t combine_threads = (int64_t)a.B * a.Hkv * a.S * a.G * 64;  // one wave per row
-  hipLaunchKernelGGL(cache_combine_kernel, dim3(grid_for(combine_threads)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -16,7 +16,9 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -384,8 +386,9 @@ hipError_t launch_prologue(const Prologue& pro, hipStream_t stream);
 
 // KV-cache attention (prefixlm_cache_bf16.hip): the key split and its workspace.
 struct CacheSplit {
-  int n_rt, splits, split_keys;
-  int64_t units;
+  int n_rt, splits;
+  int64_t groups;  // (batch row, kv head, row tile) triples
+  int64_t units;   // groups * splits workgroups
   size_t workspace_bytes;
 };
 CacheSplit cache_split(const MimirCacheAttnParams& p);

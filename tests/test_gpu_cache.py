@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 BF16 = torch.bfloat16
 
 
-def _run(device, B, S, hq, hkv, d, L, lens, causal, rows=None, cache_rows=None, seed=0):
+def _run(device, B, S, hq, hkv, d, L, lens, causal, rows=None, cache_rows=None, seed=0, index_dtype=torch.int64):
     gen = torch.Generator().manual_seed(seed)
     cache_rows = cache_rows or B
     q = torch.randn(B, S, hq, d, generator=gen).to(BF16)
@@ -28,8 +28,8 @@ def _run(device, B, S, hq, hkv, d, L, lens, causal, rows=None, cache_rows=None, 
     v = torch.randn(B, S, hkv, d, generator=gen).to(BF16)
     ck = torch.randn(cache_rows, L, hkv, d, generator=gen).to(BF16)
     cv = torch.randn(cache_rows, L, hkv, d, generator=gen).to(BF16)
-    lens_t = torch.tensor(lens, dtype=torch.int64)
-    rows_t = None if rows is None else torch.tensor(rows, dtype=torch.int64)
+    lens_t = torch.tensor(lens, dtype=index_dtype)
+    rows_t = None if rows is None else torch.tensor(rows, dtype=index_dtype)
     ck_ref, cv_ref = ck.clone(), cv.clone()
     ref = LO.attention_with_cache(q, k, v, ck_ref, cv_ref, lens_t, causal, rows_t)
 
@@ -44,9 +44,16 @@ def _run(device, B, S, hq, hkv, d, L, lens, causal, rows=None, cache_rows=None, 
 
 
 @pytest.mark.parametrize("d", [128, 64])
-def test_decode_split_keys(device, d):
+@pytest.mark.parametrize("index_dtype", [torch.int64, torch.int32])
+def test_decode_split_keys(device, d, index_dtype):
     _run(device, B=5, S=1, hq=8, hkv=2, d=d, L=1500, lens=[0, 1, 777, 1499, 64], causal=True,
-         rows=[3, 0, 6, 1, 4], cache_rows=7)
+         rows=[3, 0, 6, 1, 4], cache_rows=7, index_dtype=index_dtype)
+
+
+def test_decode_uneven_rows(device):
+    """Rows whose key ranges split into different numbers of parts (1 key to the whole cache)."""
+    _run(device, B=8, S=1, hq=16, hkv=4, d=128, L=4096, lens=[0, 63, 64, 65, 1000, 4095, 2048, 129],
+         causal=True, seed=5)
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -96,3 +103,35 @@ def test_rows_outside_the_cache_are_skipped(device):
     # batch row 0 -> cache row 1, position cache_lengths[0] = 3
     assert torch.equal(cache.keys[1, 3], k[0, 0]) and torch.equal(cache.keys[1, :3], before[1, :3])
     assert torch.equal(cache.keys[1, 4:], before[1, 4:])
+
+
+def test_repeated_calls_and_graph_replay(device):
+    """The split arrival counters are cleared by each call: back-to-back calls and replays of a
+    captured decode step (no host synchronisation, no memset) match the eager result."""
+    gen = torch.Generator().manual_seed(11)
+    B, hq, hkv, d, L = 4, 8, 2, 128, 2048
+    q = torch.randn(B, 1, hq, d, generator=gen).to(BF16).to(device)
+    k = torch.randn(B, 1, hkv, d, generator=gen).to(BF16).to(device)
+    v = torch.randn(B, 1, hkv, d, generator=gen).to(BF16).to(device)
+    cache = Cache(torch.randn(B, L, hkv, d, generator=gen).to(BF16).to(device),
+                  torch.randn(B, L, hkv, d, generator=gen).to(BF16).to(device))
+    lens = torch.tensor([5, 2000, 700, 1300], device=device)
+    first = attention_with_cache(q, k, v, cache, lens, True)
+    second = attention_with_cache(q, k, v, cache, lens, True)  # the same append again: same output
+    torch.cuda.synchronize()
+    assert torch.equal(first, second)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        attention_with_cache(q, k, v, cache, lens, True)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = attention_with_cache(q, k, v, cache, lens, True)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+        eager = attention_with_cache(q, k, v, cache, lens, True)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(eager, first)
