@@ -30,6 +30,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRows = kWaves * 32;  // query rows per workgroup
 constexpr int kKeys = 64;           // keys per tile
+constexpr int kMaxSplits = 64;      // key splits per row tile (the merge keeps one per lane)
 
 struct CacheArgs {
   const bf16_t* q;
@@ -311,32 +312,38 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
   __syncthreads();
   if (!last) return;
   // out row = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M) over the n_valid
-  // splits; one wave per row, each lane D / 64 columns.
+  // (<= 64) splits; one wave per row.  Lane c holds split c's (max, sum), the
+  // merged max and sum are wave reductions, and each lane accumulates D / 64
+  // columns over the splits with all of their loads in flight together.
+  static_assert(kMaxSplits <= 64, "one split per lane in the merge");
   const uint32_t unit0 = (uint32_t)group * a.splits;
-  const int cpl = D / 64;
+  constexpr int cpl = D / 64;
   for (int rr = wave; rr < rt_rows; rr += kWaves) {
-    float M = -INFINITY;
-    for (int c = 0; c < n_valid; ++c) {
+    float mc = -INFINITY, lc = 0.f;
+    if (lane < n_valid) {
       const f32x2 ml = __builtin_bit_cast(
-          f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, ((unit0 + c) * kRows + rr) * 8, 0, kDevScope));
-      M = fmaxf(M, ml[0]);
+          f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, ((unit0 + lane) * kRows + rr) * 8, 0, kDevScope));
+      mc = ml[0];
+      lc = ml[1];
     }
-    float lsum = 0.f, o0 = 0.f, o1 = 0.f;
-    if (M != -INFINITY) {
-      for (int c = 0; c < n_valid; ++c) {
-        const uint32_t slot = (unit0 + c) * kRows + rr;
-        const f32x2 ml = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, slot * 8, 0, kDevScope));
-        const float w = ml[0] == -INFINITY ? 0.f : fast_exp2(ml[0] - M);
-        lsum += ml[1] * w;
-        if (cpl > 1) {
-          const f32x2 o = __builtin_bit_cast(
-              f32x2, __builtin_amdgcn_raw_buffer_load_b64(ro, (slot * D + lane * 2) * 4, 0, kDevScope));
-          o0 += o[0] * w;
-          o1 += o[1] * w;
-        } else {
-          o0 += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, (slot * D + lane) * 4, 0,
-                                                                               kDevScope)) * w;
-        }
+    float M = mc;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    const float w = mc == -INFINITY ? 0.f : fast_exp2(mc - M);  // 0 for splits without allowed keys
+    float lsum = lc * w;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+    float acc[cpl] = {};
+#pragma unroll 8
+    for (int c = 0; c < n_valid; ++c) {
+      const float wc = __shfl(w, c);
+      const uint32_t off = (((unit0 + c) * kRows + rr) * D + lane * cpl) * 4;
+      if constexpr (cpl == 2) {
+        const f32x2 o = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(ro, off, 0, kDevScope));
+        acc[0] += o[0] * wc;
+        acc[1] += o[1] * wc;
+      } else {
+        acc[0] += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, off, 0, kDevScope)) * wc;
       }
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
@@ -344,8 +351,8 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
     const int ti_r = row_g / a.G;
     const int h_r = hk * a.G + (row_g - ti_r * a.G);
     bf16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)ti_r * a.o_st + (int64_t)h_r * a.o_sh + lane * cpl;
-    orow[0] = (bf16_t)(o0 * inv);
-    if (cpl > 1) orow[1] = (bf16_t)(o1 * inv);
+#pragma unroll
+    for (int i = 0; i < cpl; ++i) orow[i] = (bf16_t)(acc[i] * inv);
   }
 }
 
@@ -369,6 +376,7 @@ CacheSplit cache_split(const MimirCacheAttnParams& p) {
   int64_t splits = s.groups > 0 ? (target + s.groups - 1) / s.groups : 1;
   if (splits < 1) splits = 1;
   if (splits > tiles) splits = tiles;
+  if (splits > kMaxSplits) splits = kMaxSplits;
   s.splits = (int)splits;
   s.units = s.groups * s.splits;
   // partial O, then (max, sum) per unit row, then the arrival counters
