@@ -30,7 +30,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRows = kWaves * 32;  // query rows per workgroup
 constexpr int kKeys = 64;           // keys per tile
-constexpr int kMaxSplits = 64;      // key splits per row tile (the merge keeps one per lane)
+constexpr int kMaxSplits = 64;      // key splits per row tile
 
 struct CacheArgs {
   const bf16_t* q;
@@ -312,38 +312,43 @@ __global__ __launch_bounds__(kThreads, 2) void cache_attn_kernel(const CacheArgs
   __syncthreads();
   if (!last) return;
   // out row = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M) over the n_valid
-  // (<= 64) splits; one wave per row.  Lane c holds split c's (max, sum), the
-  // merged max and sum are wave reductions, and each lane accumulates D / 64
-  // columns over the splits with all of their loads in flight together.
-  static_assert(kMaxSplits <= 64, "one split per lane in the merge");
+  // splits, one wave per row and D / 64 columns per lane.  The splits are merged
+  // online in chunks of eight whose loads ((max, sum) and the lane's O columns)
+  // are all issued before any is used, so a chunk costs one memory round trip.
   const uint32_t unit0 = (uint32_t)group * a.splits;
   constexpr int cpl = D / 64;
+  constexpr int kChunk = 8;
   for (int rr = wave; rr < rt_rows; rr += kWaves) {
-    float mc = -INFINITY, lc = 0.f;
-    if (lane < n_valid) {
-      const f32x2 ml = __builtin_bit_cast(
-          f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, ((unit0 + lane) * kRows + rr) * 8, 0, kDevScope));
-      mc = ml[0];
-      lc = ml[1];
-    }
-    float M = mc;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-    const float w = mc == -INFINITY ? 0.f : fast_exp2(mc - M);  // 0 for splits without allowed keys
-    float lsum = lc * w;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+    float M = -INFINITY, lsum = 0.f;
     float acc[cpl] = {};
-#pragma unroll 8
-    for (int c = 0; c < n_valid; ++c) {
-      const float wc = __shfl(w, c);
-      const uint32_t off = (((unit0 + c) * kRows + rr) * D + lane * cpl) * 4;
-      if constexpr (cpl == 2) {
-        const f32x2 o = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(ro, off, 0, kDevScope));
-        acc[0] += o[0] * wc;
-        acc[1] += o[1] * wc;
-      } else {
-        acc[0] += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, off, 0, kDevScope)) * wc;
+    for (int c0 = 0; c0 < n_valid; c0 += kChunk) {
+      f32x2 ml[kChunk];
+      float ov[kChunk][cpl];
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) {
+        const uint32_t slot = (unit0 + min(c0 + i, n_valid - 1)) * kRows + rr;
+        ml[i] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(rml, slot * 8, 0, kDevScope));
+        const uint32_t off = (slot * D + lane * cpl) * 4;
+        if constexpr (cpl == 2) {
+          const f32x2 o = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(ro, off, 0, kDevScope));
+          ov[i][0] = o[0];
+          ov[i][1] = o[1];
+        } else {
+          ov[i][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, off, 0, kDevScope));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) {
+        if (c0 + i >= n_valid) break;
+        const float m = ml[i][0];
+        if (m == -INFINITY) continue;  // no allowed key in this split
+        const float m_new = fmaxf(M, m);
+        const float alpha = M == -INFINITY ? 0.f : fast_exp2(M - m_new);  // rescale the running sums
+        const float w = fast_exp2(m - m_new);
+        lsum = lsum * alpha + ml[i][1] * w;
+#pragma unroll
+        for (int j = 0; j < cpl; ++j) acc[j] = acc[j] * alpha + ov[i][j] * w;
+        M = m_new;
       }
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
