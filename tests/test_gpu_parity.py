@@ -100,6 +100,33 @@ def test_bf16_small(device, idx):
     check(case, device, label=f"small{idx}")
 
 
+def _random_shape(seed):
+    """A seeded random packing: 1-6 documents of 1..700 tokens, prefixes anywhere in [0, n]
+    (often 0 or n), GQA ratio 1/2/4/8, head_dim 64 or 128, sometimes is_causal or padding rows."""
+    g = torch.Generator().manual_seed(1000 + seed)
+    r = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))
+    ndoc = r(1, 6)
+    seq_lens = [r(1, 700) for _ in range(ndoc)]
+    prefixes = []
+    for n in seq_lens:
+        kind = r(0, 3)
+        prefixes.append(0 if kind == 0 else n if kind == 1 else r(0, n))
+    hkv = [1, 2, 4][r(0, 2)]
+    hq = hkv * [1, 2, 4, 8][r(0, 3)]
+    d = [64, 128][r(0, 1)]
+    pad = sum(seq_lens) + r(0, 70) if r(0, 2) == 0 else None
+    return seq_lens, prefixes, hq, hkv, d, pad, r(0, 4) == 0
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_bf16_random_shapes(device, seed):
+    """Seeded random shapes (the edge cases above are hand-picked; these are not)."""
+    seq_lens, prefixes, hq, hkv, d, pad_to, causal = _random_shape(seed)
+    case = make_case(seq_lens, prefixes, hq, hkv, d, seed=seed, dtype=torch.bfloat16, pad_to=pad_to,
+                     is_causal=causal)
+    check(case, device, label=f"random{seed} hq={hq} hkv={hkv} d={d} causal={causal} pad={pad_to}")
+
+
 @pytest.mark.parametrize("idx", [0, 1, 2, 4, 5, 6, 8])
 def test_f32_small(device, idx):
     seq_lens, prefixes, hq, hkv, d, pad_to, causal = SMALL[idx]
