@@ -306,7 +306,7 @@ struct PlanArgs {
   const int32_t* prefix_lens;
   int numseqs, total_seqlen, is_causal, T, kind, group, cap;
   void* items;     // int2 [cap] (kind 0) or int4 [cap] (kind 1)
-  // kind 1: split items costing more than (total cost * split_heads / slots) / 3,
+  // kind 1: split items costing more than (total cost * split_heads / slots) / 2,
   // heaviest first and whole cost buckets at a time, up to max_pairs items;
   // split_heads = 0 disables splitting.
   int split_heads, max_pairs, slots;

@@ -209,8 +209,8 @@ __device__ void plan_block(const PlanArgs& a) {
   __syncthreads();
   const double mine = walk_items<false>(a, sm, 0x7fffffff);
   double threshold = 0.0;
-  if (split)  // a third of the average per compute unit
-    threshold = block_sum(mine, sm) * a.split_heads / a.slots / 3.0;
+  if (split)  // half the average per compute unit
+    threshold = block_sum(mine, sm) * a.split_heads / a.slots / 2.0;
   int total = bucket_starts(sm, threshold, split ? a.max_pairs : 0);
   const int cut = sm.cut;
   if (cut != 0x7fffffff) {  // recount with the heavy items halved
