@@ -46,6 +46,7 @@ struct BwdArgs {
 // Each launcher computes its own grid from the geometry in `a` and enqueues one
 // kernel on `stream`.
 hipError_t launch_bwd_dq_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all, hipStream_t stream);
+// head_dim 64 (prefixlm_bwd_dkdv_bf16.hip)
 hipError_t launch_bwd_dkdv_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all,
                                 hipStream_t stream);
 // head_dim 128, two waves per SIMD (prefixlm_bwd_dkdv_pair_bf16.hip)

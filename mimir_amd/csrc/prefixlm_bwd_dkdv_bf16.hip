@@ -1,5 +1,6 @@
-// bf16 prefix-LM attention backward, dK / dV kernel, for gfx950 (MI355X).
-// Owner = (kv head, key tile); see prefixlm_bwd_bf16.hip for the split.
+// bf16 prefix-LM attention backward, dK / dV kernel for head_dim 64, for gfx950
+// (MI355X); head_dim 128 uses prefixlm_bwd_dkdv_pair_bf16.hip.  Owner = (kv
+// head, key tile); see prefixlm_bwd_bf16.hip for the split.
 #include "prefixlm_bwd_bf16.h"
 
 namespace mimir {
@@ -14,15 +15,15 @@ namespace {
 // Workgroup r * Hkv + h takes kv head h of entry r of the key-tile work list
 // (prefixlm_prologue.hip): the heaviest key tiles first.
 //
-// At head_dim 128 the K / V fragments and the dK / dV accumulators allow one
-// wave per SIMD, so LDS latency is hidden inside the wave: every operand
-// fragment is read one phase ahead (see compute below).
+// Two workgroups per CU (two waves per SIMD); every operand fragment is read
+// one phase ahead of its MFMAs (see compute below).
 // ---------------------------------------------------------------------------
 template <int D>
 struct DkCfg {
+  static_assert(D == 64, "head_dim 128 uses the pair kernel");
   static constexpr int kWaves = 4;                    // waves per workgroup, 32 keys each
   static constexpr int kKeys = 32 * kWaves;           // keys per workgroup
-  static constexpr int kWavesPerSimd = D <= 64 ? 2 : 1;
+  static constexpr int kWavesPerSimd = 2;
 };
 
 template <int D>
@@ -272,8 +273,7 @@ hipError_t launch_bwd_dkdv_bf16(const BwdArgs& a, int head_dim, int numseqs, int
                                 hipStream_t stream) {
   switch (head_dim) {
     case 64: return launch<64>(a, numseqs, max_seqlen_all, stream);
-    case 128: return launch<128>(a, numseqs, max_seqlen_all, stream);
-    default: return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;  // head_dim 128: launch_bwd_dkdv_pair_bf16
   }
 }
 
