@@ -111,3 +111,34 @@ def test_work_accounting_matches_baseline_table():
 def test_package_exports():
     for name in mimir_amd.__all__:
         assert hasattr(mimir_amd, name)
+
+
+def test_cache_attention_argument_checks_on_cpu():
+    """attention_with_cache (layers.py:134-167) checks dtype and shapes before anything runs, and CPU
+    tensors raise instead of falling back."""
+    from mimir_amd.cache import Cache, attention_with_cache
+    bf = torch.bfloat16
+    q = torch.zeros(2, 1, 8, 64, dtype=bf)
+    k = torch.zeros(2, 1, 2, 64, dtype=bf)
+    cache = Cache.create(2, 16, 2, 64, dtype=bf)
+    assert cache.keys.shape == (2, 16, 2, 64) and cache.values.dtype == bf and not cache.keys.any()
+    lens = torch.tensor([3, 0])
+    with pytest.raises(TypeError):
+        attention_with_cache(q.float(), k.float(), k.float(), Cache.create(2, 16, 2, 64), lens, True)
+    with pytest.raises(ValueError):  # key / value shapes differ from the query's batch and tokens
+        attention_with_cache(q, k[:1], k[:1], cache, lens, True)
+    with pytest.raises(ValueError):  # Hq not a multiple of Hkv
+        attention_with_cache(torch.zeros(2, 1, 3, 64, dtype=bf), k, k, cache, lens, True)
+    with pytest.raises(ValueError):  # cache head_dim differs
+        attention_with_cache(q, k, k, Cache.create(2, 16, 2, 32, dtype=bf), lens, True)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        attention_with_cache(q, k, k, cache, lens, True)
+
+
+def test_layer_core_cpu_tensors_raise():
+    """The fused layer core (layers.py:182-239) and the RoPE kernel have no CPU fallback either."""
+    from mimir_amd import rope
+    x = torch.zeros(4, 2, 64, dtype=torch.bfloat16)
+    cs = torch.ones(4, 64)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        rope(x, cs, cs)
