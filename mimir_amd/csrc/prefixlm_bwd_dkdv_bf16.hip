@@ -76,27 +76,45 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(
       a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh, rows_bytes(g.n, a.v_st, D));
 
-  // Iteration it covers q head hk * G + it / nqt and query tile it % nqt.
+  // Iteration it covers q head hk * G + it / nqt and query tile it % nqt.  The
+  // tile copies walk that order with running addresses (adds only, no division
+  // per tile).
   const TileLoader<D, kDkWaves> ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane);
-  auto issue = [&](int it, bf16_t* tq, bf16_t* to, float* tl, float* td) {
-    const int hh = it / nqt;
-    const int qb = q_begin + (it - hh * nqt) * kBwdBlockQT;
-    const int h = hk * a.group + hh;
-    ldq.issue(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, qb, g.nq, tq);
-    ldo.issue(a.dout + (int64_t)g.start * a.do_st + (int64_t)h * a.do_sh, qb, g.nq, to);
-    if (wave == 0) {
-      const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse2 + (int64_t)h * a.T + g.start, (uint32_t)g.nq * 4u);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (__attribute__((address_space(3))) void*)tl, 4,
-                                               (uint32_t)(qb + lane) * 4u, 0, 0, 0);
+  const uint32_t q_st32 = (uint32_t)a.q_st, o_st32 = (uint32_t)a.do_st;
+  const int qh0 = hk * a.group;
+  const bf16_t* q_head = a.q + ((int64_t)g.start + q_begin) * a.q_st + (int64_t)qh0 * a.q_sh;
+  const bf16_t* o_head = a.dout + ((int64_t)g.start + q_begin) * a.do_st + (int64_t)qh0 * a.do_sh;
+  // one 4-byte row per wave: wave 0 lse2, the others delta (same data to the same place)
+  const float* r_head = (wave == 0 ? a.lse2 : a.delta) + (int64_t)qh0 * a.T + g.start + q_begin;
+  const bf16_t* i_q = q_head;
+  const bf16_t* i_o = o_head;
+  const float* i_r = r_head;
+  int i_qt = 0, i_rows = g.nq - q_begin;
+  auto issue_next = [&](bf16_t* tq, bf16_t* to, float* tl, float* td) {
+    ldq.issue_at(i_q, rows_bytes32(i_rows, q_st32, D), tq);
+    ldo.issue_at(i_o, rows_bytes32(i_rows, o_st32, D), to);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(i_r, i_rows > 0 ? (uint32_t)i_rows * 4u : 0u);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(wave == 0 ? tl : td), 4,
+                                             (uint32_t)lane * 4u, 0, 0, 0);
+    if (++i_qt == nqt) {
+      i_qt = 0;
+      i_rows = g.nq - q_begin;
+      q_head += a.q_sh;
+      o_head += a.do_sh;
+      r_head += a.T;
+      i_q = q_head;
+      i_o = o_head;
+      i_r = r_head;
     } else {
-      const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.delta + (int64_t)h * a.T + g.start, (uint32_t)g.nq * 4u);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (__attribute__((address_space(3))) void*)td, 4,
-                                               (uint32_t)(qb + lane) * 4u, 0, 0, 0);
+      i_rows -= kBwdBlockQT;
+      i_q += kBwdBlockQT * a.q_st;
+      i_o += kBwdBlockQT * a.do_st;
+      i_r += kBwdBlockQT;
     }
   };
   // Three LDS stages: iteration it computes on stage it % 3 while the tiles of
   // it + 1 and it + 2 are in flight.
-  if (n_iter > 0) issue(0, sQ0, sO0, sL0, sD0);
+  if (n_iter > 0) issue_next(sQ0, sO0, sL0, sD0);
 
   bf16x8 kf[KS], vf[KS];
 #pragma unroll
@@ -105,7 +123,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
     kf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
     vf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rv, (uint32_t)((key * a.v_st + 16 * ks + 8 * hi) * 2)));
   }
-  if (n_iter > 1) issue(1, sQ1, sO1, sL1, sD1);
+  if (n_iter > 1) issue_next(sQ1, sO1, sL1, sD1);
   // Buffer loads per issue() and wave: Q and dO tiles plus one lse2 / delta row.
   constexpr int kLoadsPerIssue = 2 * TileLoader<D, kDkWaves>::kPerWave + 1;
   auto sync_stage = [&](int it) {  // tile `it` has landed everywhere; tile it + 1 may still be in flight
@@ -212,9 +230,10 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto step = [&](int it, const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
-    const int hh = it / nqt;
-    const int qb = q_begin + (it - hh * nqt) * kBwdBlockQT;
+  int s_qt = 0;  // query tile of the next step (the head only matters to the copies)
+  auto step = [&](const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
+    const int qb = q_begin + s_qt * kBwdBlockQT;
+    if (++s_qt == nqt) s_qt = 0;
     if (!wave_active || qb + kBwdBlockQT <= w_qs_min) return;
     compute((qb < w_qs_max) || (qb + kBwdBlockQT > g.nq), qb, sQ, sdO, sL, sD);
   };
@@ -223,16 +242,16 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   // whose stage ((it + 2) % 3) then receives tile it + 2.
   for (int it = 0; it < n_iter; it += 3) {
     sync_stage(it);
-    if (it + 2 < n_iter) issue(it + 2, sQ2, sO2, sL2, sD2);
-    step(it, sQ0, sO0, sL0, sD0);
+    if (it + 2 < n_iter) issue_next(sQ2, sO2, sL2, sD2);
+    step(sQ0, sO0, sL0, sD0);
     if (it + 1 >= n_iter) break;
     sync_stage(it + 1);
-    if (it + 3 < n_iter) issue(it + 3, sQ0, sO0, sL0, sD0);
-    step(it + 1, sQ1, sO1, sL1, sD1);
+    if (it + 3 < n_iter) issue_next(sQ0, sO0, sL0, sD0);
+    step(sQ1, sO1, sL1, sD1);
     if (it + 2 >= n_iter) break;
     sync_stage(it + 2);
-    if (it + 4 < n_iter) issue(it + 4, sQ1, sO1, sL1, sD1);
-    step(it + 2, sQ2, sO2, sL2, sD2);
+    if (it + 4 < n_iter) issue_next(sQ1, sO1, sL1, sD1);
+    step(sQ2, sO2, sL2, sD2);
   }
 
   if (!wave_active) return;
