@@ -257,6 +257,8 @@ struct TileLanes {
 
 // s_waitcnt vmcnt(0) (GFX9 encoding: expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt left at their maxima).
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 // Wait until at most N vector-memory operations of this wave are outstanding
 // (they complete in issue order, so everything older than the last N is done).
 template <int N>
@@ -386,6 +388,7 @@ hipError_t launch_prologue(const Prologue& pro, hipStream_t stream);
 
 // KV-cache attention (prefixlm_cache_bf16.hip): the key split and its workspace.
 struct CacheSplit {
+  bool decode;     // at most 32 query rows per kv head: the decode kernel
   int n_rt, splits;
   int64_t groups;  // (batch row, kv head, row tile) triples
   int64_t units;   // groups * splits workgroups

@@ -50,6 +50,13 @@ def test_decode_split_keys(device, d, index_dtype):
          rows=[3, 0, 6, 1, 4], cache_rows=7, index_dtype=index_dtype)
 
 
+@pytest.mark.parametrize("S,causal", [(3, True), (4, True), (4, False), (5, True)])
+def test_short_chunks_around_the_decode_kernel(device, S, causal):
+    """S * G <= 32 query rows per kv head take the decode kernel (each wave its own key tiles,
+    merged through LDS), 40 rows the row-tile kernel; causal masks per token."""
+    _run(device, B=3, S=S, hq=16, hkv=2, d=128, L=900, lens=[0, 451, 880], causal=causal, seed=20 + S)
+
+
 def test_decode_uneven_rows(device):
     """Rows whose key ranges split into different numbers of parts (1 key to the whole cache)."""
     _run(device, B=8, S=1, hq=16, hkv=4, d=128, L=4096, lens=[0, 63, 64, 65, 1000, 4095, 2048, 129],
