@@ -361,8 +361,8 @@ def main() -> int:
                          "HBM traffic for scaling the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build runs the kernel on one "
-              "GPU's share of the workload; multi-GPU sharding is described in DESIGN.md, not launched.",
+        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): the operator runs on one GPU's "
+              "share of the workload; sharding it over GPUs (documents and heads, no exchange) is not launched here.",
               file=sys.stderr)
         return 2
 
