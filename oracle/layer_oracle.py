@@ -1,7 +1,8 @@
 """CPU oracle for the attention layer's core around prefix-LM attention.
 
-TEST INFRASTRUCTURE ONLY.  Only ``tests/`` may import this module, as the
-checker of ``mimir_amd.layer``; the product path never imports it.
+TEST INFRASTRUCTURE ONLY.  Only ``tests/`` may import this module, as what the
+results of ``mimir_amd.layer`` and ``mimir_amd.cache`` are compared against; the
+product path never imports it.
 
 Restates src/mimir/model/layers.py: ``rotate_half`` / ``apply_rotary_pos_emb``
 (layers.py:24-40), the gqkv head split (layers.py:182-184), the RoPE calls

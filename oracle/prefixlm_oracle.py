@@ -1,9 +1,9 @@
 """CPU oracle for Mimir2 prefix-LM attention.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
-checker (or, for the baseline, as the timed CPU restatement of the reference's
-masked-SDPA path).  The product path (``mimir_amd``) never imports it: it runs
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as what
+the kernels' results are compared against (or, for the baseline, as the timed
+CPU restatement of the reference's masked-SDPA path).  The product path (``mimir_amd``) never imports it: it runs
 the HIP library or raises.
 
 Every function restates the reference algorithm it cites.  The reference is
