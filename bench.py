@@ -119,6 +119,20 @@ def cpu_baseline(case, target_seconds: float = 12.0, unit_bytes_cap: float = 3e9
     }
 
 
+def dscore_blocks(case) -> int:
+    """32 x 32 (query, key) blocks per head holding at least one attended pair: the dS
+    blocks the dK / dV kernel stores and the dQ kernel reads with the score-gradient hand-off."""
+    cu = case.cu_seqlens.tolist()
+    pl = case.prefix_lens.tolist()
+    total = 0
+    for s in range(int(case.numseqs)):
+        n = cu[s + 1] - cu[s]
+        p = 0 if case.is_causal else min(max(pl[s], 0), n)
+        for qa in range(0, n, 32):
+            total += (max(p, min(qa + 32, n)) + 31) // 32
+    return total
+
+
 def _measured_traffic(workload: str, kernel: str):
     """HBM bytes per launch of ``kernel`` on ``workload`` from the committed PMC summary.
 
@@ -459,9 +473,11 @@ def main() -> int:
     value = flops / (ms_per_step * 1e-3) / 1e12
     peak = PEAK_F32_TFLOPS if c.q.dtype == torch.float32 else PEAK_BF16_TFLOPS
     kernel_flops = {"fwd": f_fwd, "dkdv": 8.0 * d * hq * pairs, "dq": 2.0 * d * hq * pairs}
+    handoff = not fwd_only and int(lib.mimir_prefixlm_bwd_dscore_bytes(bpr)) > 0  # dQ reads dK/dV's dS
     kernel_names = {"fwd": "fwd_bf16_kernel" if elem == 2 else "fwd_f32_kernel",
-                    "dkdv": "dkdv_pair_kernel" if (elem == 2 and d == 128) else "dkdv_kernel",
-                    "dq": "dq_kernel"}
+                    "dkdv": ("dkdv_pair_ds_kernel" if handoff else "dkdv_pair_kernel") if (elem == 2 and d == 128)
+                    else "dkdv_kernel",
+                    "dq": "dq_ds_kernel" if handoff else "dq_kernel"}
     dom = max((n for n in kernel_flops if n in stage_avg), key=lambda n: stage_avg[n])
     achieved = kernel_flops[dom] / (stage_avg[dom] * 1e-3) / 1e12
     alg_bytes = fwd_bytes(T, hq, hkv, d, elem) + (0 if fwd_only else bwd_bytes(T, hq, hkv, d, elem))
@@ -509,6 +525,13 @@ def main() -> int:
         res["roofline"]["traffic_source"] = measured["source"]
     if not fwd_only:
         res["bwd_tflops"] = round(f_bwd / ((ms_per_step - stage_avg["fwd"]) * 1e-3) / 1e12, 2)
+    res["dscore_handoff"] = handoff
+    if handoff:
+        # the dQ kernel is then HBM-bound: it streams every stored dS block once
+        # (plus K once and the dQ rows)
+        ds_bytes = dscore_blocks(case) * hq * 2048 + T * (hkv + hq) * d * elem
+        res["dq_ds_bytes"] = ds_bytes
+        res["dq_ds_gbs"] = round(ds_bytes / (stage_avg["dq"] * 1e-3) / 1e9, 1)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(case)
     print(json.dumps(res), flush=True)

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MIMIR_PREFIXLM_ABI_VERSION 3
+#define MIMIR_PREFIXLM_ABI_VERSION 4
 
 /* Element types of q/k/v/out/dout/dq/dk/dv (lse and the workspace are float32). */
 enum MimirDType {
@@ -143,6 +143,13 @@ typedef struct MimirPrefixLMBwdParams {
   int64_t gate_stride_token, gate_stride_head;
   void* dgate;                /* [T, Hq, D]; required with a gate */
   int64_t dgate_stride_token, dgate_stride_head;
+  /* Score-gradient hand-off (bf16, head_dim 128; no reference counterpart): when
+   * the bf16 dS tiles of every (q head, 32-query block, 32-key block) fit in
+   * this many bytes of workspace (mimir_prefixlm_bwd_dscore_bytes), the DKDV
+   * stage writes them there and the DQ stage computes dQ = dS K from them
+   * instead of recomputing S and dP; DQ then reads what DKDV wrote and runs
+   * after it.  0: DQ recomputes. */
+  size_t dscore_limit_bytes;
 } MimirPrefixLMBwdParams;
 
 /* Bytes of device workspace the forward needs: the heaviest-first tile work list
@@ -165,7 +172,8 @@ int mimir_prefixlm_bwd(const MimirPrefixLMBwdParams* params, void* stream);
 /* Backward stages, for callers that schedule them themselves (e.g. dK/dV and
  * dQ on two streams once delta is done).  mimir_prefixlm_bwd runs them all, in
  * order.  DELTA must complete before DKDV and DQ; DKDV, DQ and FILL are
- * independent of each other.  No reference counterpart: the reference exposes
+ * independent of each other, except that with the score-gradient hand-off
+ * (mimir_prefixlm_bwd_dscore_bytes non-zero) DQ reads what DKDV wrote.  No reference counterpart: the reference exposes
  * the backward only through autograd (flash_attention_prefixlm_v2.py:270-283). */
 enum MimirBwdStage {
   MIMIR_BWD_STAGE_DELTA = 1, /* delta = rowsum(O * dO), lse * log2(e) and the tile work lists into the workspace */
@@ -186,9 +194,16 @@ size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_he
                                           int32_t max_seqlen_all);
 
 /* Bytes of backward workspace for these parameters: mimir_prefixlm_bwd_workspace_bytes
- * plus, with a gate, the attention's upstream gradient [T, Hq, D] in the element type.
- * Only the size fields, head_dim, dtype and gate are read. */
+ * plus, with a gate, the attention's upstream gradient [T, Hq, D] in the element type,
+ * plus the score-gradient tiles when mimir_prefixlm_bwd_dscore_bytes(params) is non-zero.
+ * Only the size fields, head_dim, dtype, gate and dscore_limit_bytes are read. */
 size_t mimir_prefixlm_bwd_workspace_size(const MimirPrefixLMBwdParams* params);
+
+/* Bytes of workspace the score-gradient hand-off takes for these parameters, 0
+ * when it is off: bf16 with head_dim 128 only, and only when the bf16 tiles,
+ * Hq x (floor(T / 32) + numseqs + 1) x ceil(max_seqlen_all / 32) blocks of
+ * 32 x 32, fit in dscore_limit_bytes.  No reference counterpart. */
+size_t mimir_prefixlm_bwd_dscore_bytes(const MimirPrefixLMBwdParams* params);
 
 /* Rotary position embedding on [T, H, D] rows, rotate-half convention
  * (reference: src/mimir/model/layers.py:24-40, apply_rotary_pos_emb on the q / k

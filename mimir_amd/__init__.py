@@ -20,6 +20,7 @@ from .prefixlm import (
     flash_attn_varlen_prefixlm,
     prefixlm_attn_bwd,
     prefixlm_attn_fwd,
+    set_dscore_workspace_limit,
     set_validate_metadata,
 )
 
@@ -35,5 +36,6 @@ __all__ = [
     "prefixlm_attn_fwd",
     "prefixlm_seq_info_from_tensors",
     "rope",
+    "set_dscore_workspace_limit",
     "set_validate_metadata",
 ]

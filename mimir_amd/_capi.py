@@ -16,7 +16,7 @@ from pathlib import Path
 
 # MIMIR_PREFIXLM_LIB overrides the in-tree library (e.g. to A/B two builds).
 LIB_PATH = Path(os.environ.get("MIMIR_PREFIXLM_LIB") or Path(__file__).resolve().parent / "_lib" / "libmimir_prefixlm.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_FLOAT32 = 0
 DTYPE_BFLOAT16 = 1
@@ -70,6 +70,7 @@ class BwdParams(ctypes.Structure):
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("gate", _vp), ("gate_stride_token", _i64), ("gate_stride_head", _i64),
         ("dgate", _vp), ("dgate_stride_token", _i64), ("dgate_stride_head", _i64),
+        ("dscore_limit_bytes", ctypes.c_size_t),
     ]
 
 
@@ -113,6 +114,7 @@ EXPORTED_SYMBOLS = (
     "mimir_prefixlm_fwd_workspace_bytes",
     "mimir_prefixlm_bwd_workspace_bytes",
     "mimir_prefixlm_bwd_workspace_size",
+    "mimir_prefixlm_bwd_dscore_bytes",
     "mimir_prefixlm_rope",
     "mimir_prefixlm_cache_attn",
     "mimir_prefixlm_cache_attn_workspace_bytes",
@@ -155,6 +157,8 @@ def load() -> ctypes.CDLL:
         lib.mimir_prefixlm_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mimir_prefixlm_bwd_workspace_size.argtypes = [ctypes.POINTER(BwdParams)]
         lib.mimir_prefixlm_bwd_workspace_size.restype = ctypes.c_size_t
+        lib.mimir_prefixlm_bwd_dscore_bytes.argtypes = [ctypes.POINTER(BwdParams)]
+        lib.mimir_prefixlm_bwd_dscore_bytes.restype = ctypes.c_size_t
         lib.mimir_prefixlm_rope.argtypes = [ctypes.POINTER(RopeParams), _vp]
         lib.mimir_prefixlm_rope.restype = ctypes.c_int
         lib.mimir_prefixlm_cache_attn.argtypes = [ctypes.POINTER(CacheAttnParams), _vp]

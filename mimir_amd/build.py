@@ -42,6 +42,7 @@ SOURCES = [
     "prefixlm_fwd_bf16.hip",
     "prefixlm_bwd_bf16.hip",
     "prefixlm_bwd_dq_bf16.hip",
+    "prefixlm_bwd_dq_ds_bf16.hip",
     "prefixlm_bwd_dkdv_bf16.hip",
     "prefixlm_bwd_dkdv_pair_bf16.hip",
     "prefixlm_f32.hip",

@@ -38,6 +38,8 @@ struct BwdArgs {
   int* split_ctr;    // workspace: arrival counter per (pair, kv head)
   int* queue;        // workspace: [0] next unit, [1] finished workgroups (dK / dV work queue)
   float* split_buf;  // workspace: two kSplitSlotFloats slots per (pair, kv head)
+  bf16_t* dscore;    // workspace: bf16 dS blocks (dscore_geometry), NULL: dQ recomputes
+  int ds_rows, ds_width;
   float scale;
   float scale_log2;
 };
@@ -46,6 +48,8 @@ struct BwdArgs {
 // Each launcher computes its own grid from the geometry in `a` and enqueues one
 // kernel on `stream`.
 hipError_t launch_bwd_dq_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all, hipStream_t stream);
+// head_dim 128, dQ from the score gradients the dK / dV stage stored (prefixlm_bwd_dq_ds_bf16.hip)
+hipError_t launch_bwd_dq_ds_bf16(const BwdArgs& a, int numseqs, hipStream_t stream);
 // head_dim 64 (prefixlm_bwd_dkdv_bf16.hip)
 hipError_t launch_bwd_dkdv_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all,
                                 hipStream_t stream);

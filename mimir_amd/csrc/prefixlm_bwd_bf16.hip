@@ -7,6 +7,8 @@
 //   dq:     owner = (query head, 128 query rows).  Per 64-key tile:
 //             S^T = K Q^T, dP^T = V dO^T, P^T = exp(scale*S^T - lse),
 //             dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T.
+//           With the score-gradient hand-off (head_dim 128) the dK/dV kernel
+//           stores its bf16 dS tiles and dQ^T += K^T dS^T reads them instead.
 //   dkdv:   owner = (kv head, key tile).  Per q-head of the GQA group and per
 //           64-query tile:  S = Q K^T, dP = dO V^T, P, dS as above,
 //             dV^T += dO^T P,  dK^T += Q^T dS.
@@ -42,9 +44,14 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   a.dk = (bf16_t*)p.dk;
   a.dv = (bf16_t*)p.dv;
   const bool gated = p.gate != nullptr;
+  const size_t ds_bytes = mimir_prefixlm_bwd_dscore_bytes(&p);
   const BwdWorkspace ws = bwd_workspace_layout(p.total_tokens, p.num_q_heads, p.numseqs, p.max_seqlen_all,
-                                               gated ? (size_t)p.total_tokens * p.num_q_heads * D * 2 : 0);
+                                               gated ? (size_t)p.total_tokens * p.num_q_heads * D * 2 : 0, ds_bytes);
   char* const wsb = (char*)p.workspace;
+  const DscoreGeom dsg = dscore_geometry(p.total_tokens, p.num_q_heads, p.numseqs, p.max_seqlen_all);
+  a.dscore = ds_bytes > 0 ? (bf16_t*)(wsb + ws.dscore) : nullptr;
+  a.ds_rows = dsg.rows;
+  a.ds_width = dsg.width;
   a.delta = (float*)(wsb + ws.delta);
   a.lse2 = (float*)(wsb + ws.lse2);
   a.plan_q = (int2*)(wsb + ws.plan_q);
@@ -112,7 +119,9 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   // dK/dV (head_dim 128) runs as one persistent workgroup per CU; dQ, launched
   // behind it on a second stream, takes over each CU as its dK/dV workgroup
   // finishes and so fills the dK/dV tail.  The join makes `stream` wait for both.
-  const bool both = D == 128 && (stages & MIMIR_BWD_STAGE_DKDV) && (stages & MIMIR_BWD_STAGE_DQ);
+  // With the score-gradient hand-off dQ reads what dK/dV wrote: one stream, in order.
+  const bool both = D == 128 && a.dscore == nullptr && (stages & MIMIR_BWD_STAGE_DKDV) &&
+                    (stages & MIMIR_BWD_STAGE_DQ);
   SideStream* ss = both ? side_stream() : nullptr;
   if (ss != nullptr) {
     if ((e = hipEventRecord(ss->fork, stream)) != hipSuccess) return e;

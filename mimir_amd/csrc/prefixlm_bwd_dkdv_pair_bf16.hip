@@ -14,16 +14,22 @@
 // the 128 x 128 V tile is staged in LDS once and read as the B operand of dP.
 // With two waves per SIMD the hardware overlaps one wave's softmax with the
 // other's MFMAs.
+//
+// dkdv_pair_ds_kernel also stores each step's bf16 dS (32 queries x the wave's
+// 32 keys, one 2 KiB block, dscore_geometry in prefixlm_common.h) for the dQ
+// stage, which then needs no recompute of S and dP.
 #include "prefixlm_bwd_bf16.h"
 
 namespace mimir {
 namespace {
 
 constexpr int kPairWaves = 8;
+constexpr int kNonTemporal = 2;  // buffer cache policy: streaming (nt)
 constexpr int kPairKeys = 128;
 constexpr int kPairD = 128;
 
-__global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const BwdArgs a) {
+template <bool kStoreDs>
+__device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   constexpr int D = kPairD;
   constexpr int DT = D / 32;
   constexpr int KS = D / 16;
@@ -93,6 +99,9 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   const int n_iter = (half == 1 ? n_all / 2 : n_all) - it_lo;
   const int head0 = nqt > 0 ? it_lo / nqt : 0;  // first step: q head hk * G + head0, query tile tile0
   const int tile0 = it_lo - head0 * nqt;
+  // dS blocks of this wave: key block ka / 32 of block row floor(start / 32) + s + query / 32
+  const int ds_row0 = g.start / kDsBlock + s;
+  const bool ds_key_ok = (ka >> 5) < a.ds_width;
 
   const bf16_t* kseq = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
   const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
@@ -163,8 +172,8 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   // B operand of dP: V rows of this slice
   const bf16_t* const sVs = sV + (slice >> 1) * L::kElems + tl.op_base + (slice & 1) * 32 * L::kRowElems;
 
-  auto compute = [&](bool masked, int qr, const bf16_t* sQ, const bf16_t* sdO, const float* sL,
-                     const float* sD) {  // qr = first query row of this wave's half
+  auto compute = [&](bool masked, int qr, int head, const bf16_t* sQ, const bf16_t* sdO, const float* sL,
+                     const float* sD) {  // qr = first query row of this wave's half, head = q head in the group
     f32x16 sc = f32x16{}, dp = f32x16{};
     // Per-step copies of the lane offsets: recomputing the stage addresses from
     // them each step keeps one register per offset live instead of one per
@@ -236,10 +245,28 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
         if (base + (unsigned)(8 * (r >> 2) + (r & 3)) >= lim) sc[r] = -INFINITY;
     }
     bf16x8 pb[2], db[2];
+    // dS half s2 (positions 16 s2 .. + 15 of the block: 1 KiB of 32 key rows
+    // of 32 bytes) to key row l32, positions 16 s2 + 8 hi + 0..7: one store
+    // instruction writes 1 KiB contiguously, non-temporal (cache policy nt), so
+    // the stream of dS does not push the Q / dO tiles other workgroups reuse out
+    // of L2.  The stores join the vmcnt queue behind the tile copies in flight,
+    // so the stage waits stay conservative.
+    __amdgpu_buffer_rsrc_t rds;
+    if constexpr (kStoreDs) {
+      const int row = ds_row0 + (qr >> 5);
+      const int64_t blk = ((int64_t)(hk * a.group + head) * a.ds_rows + row) * a.ds_width + (ka >> 5);
+      rds = make_rsrc(a.dscore + blk * kDsBlockElems, ds_key_ok && row < a.ds_rows ? kDsBlockElems * 2 : 0);
+    }
+    auto store_ds = [&](int s2) {
+      if constexpr (kStoreDs)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, db[s2]), rds,
+                                               (uint32_t)(s2 * 1024 + l32 * 32 + hi * 16), 0, kNonTemporal);
+    };
     softmax(0, 0);
     softmax(0, 1);
     pb[0] = to_bf16x8(tp);
     db[0] = to_bf16x8(tds);
+    store_ds(0);
     rd_ld(1);
     // Eight dV / dK MFMA pairs; the softmax of the second 16-query step runs
     // beside the first four.
@@ -255,15 +282,20 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
       if (j == 3) {
         pb[1] = to_bf16x8(tp);
         db[1] = to_bf16x8(tds);
+        store_ds(1);
       }
     }
   };
-  int s_qt = tile0;  // query tile of the next step (the head only matters to the copies)
+  int s_qt = tile0, s_head = head0;  // query tile and q head of the next step
   auto step = [&](const bf16_t* sQ, const bf16_t* sdO, const float* sL, const float* sD) {
     const int qr = q_begin + s_qt * kBwdBlockQT + 32 * qh;
-    if (++s_qt == nqt) s_qt = 0;
+    const int head = s_head;
+    if (++s_qt == nqt) {
+      s_qt = 0;
+      ++s_head;
+    }
     if (!wave_active || qr + 32 <= w_qs_min || qr >= g.nq) return;
-    compute(qr < w_qs_max || qr + 32 > g.nq, qr, sQ, sdO, sL, sD);
+    compute(qr < w_qs_max || qr + 32 > g.nq, qr, head, sQ, sdO, sL, sD);
   };
 
   // After the barrier of iteration it every wave is done with iteration it - 1,
@@ -443,6 +475,13 @@ __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const Bwd
   }
 }
 
+__global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const BwdArgs a) {
+  dkdv_pair_body<false>(a);
+}
+__global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_ds_kernel(const BwdArgs a) {
+  dkdv_pair_body<true>(a);
+}
+
 }  // namespace
 
 hipError_t launch_bwd_dkdv_pair_bf16(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
@@ -453,8 +492,8 @@ hipError_t launch_bwd_dkdv_pair_bf16(BwdArgs a, int numseqs, int max_seqlen_all,
   // one persistent workgroup per CU
   const int64_t units = (int64_t)a.cap_k * a.Hkv;
   const int grid = (int)(units < device_cu_count() ? units : device_cu_count());
-  hipLaunchKernelGGL(dkdv_pair_kernel, dim3((unsigned)grid), dim3(kPairWaves * 64), 0,
-                     stream, a);
+  hipLaunchKernelGGL(a.dscore != nullptr ? dkdv_pair_ds_kernel : dkdv_pair_kernel, dim3((unsigned)grid),
+                     dim3(kPairWaves * 64), 0, stream, a);
   return hipGetLastError();
 }
 

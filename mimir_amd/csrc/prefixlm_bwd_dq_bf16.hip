@@ -175,7 +175,6 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
     }
 }
 
-
 template <int D>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   static_assert(kBlockQ == kPlanTile, "work-list tiles are the dQ query tiles");
@@ -185,9 +184,11 @@ hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream
   return hipGetLastError();
 }
 
+
 }  // namespace
 
 hipError_t launch_bwd_dq_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all, hipStream_t stream) {
+  if (head_dim == 128 && a.dscore != nullptr) return launch_bwd_dq_ds_bf16(a, numseqs, stream);
   switch (head_dim) {
     case 64: return launch<64>(a, numseqs, max_seqlen_all, stream);
     case 128: return launch<128>(a, numseqs, max_seqlen_all, stream);

@@ -1,0 +1,163 @@
+// bf16 prefix-LM attention backward, dQ from the stored score gradients, for
+// gfx950 (MI355X).  Owner = (query head, 128 query rows), as in
+// prefixlm_bwd_dq_bf16.hip; see prefixlm_bwd_bf16.hip for the split.
+#include "prefixlm_bwd_bf16.h"
+
+namespace mimir {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kBlockQ = 128;  // query rows per workgroup (32 per wave)
+constexpr int kBlockK = 64;   // keys per LDS tile
+constexpr int kNonTemporal = 2;  // buffer cache policy: streaming (nt), for dS read once
+
+// ---------------------------------------------------------------------------
+// dQ from the stored score gradients (head_dim 128): dQ^T += K^T dS^T with dS
+// read from the blocks the dK / dV kernel wrote (dscore_geometry in
+// prefixlm_common.h) instead of recomputed.  Same owner, work list and K tiles
+// as dq_kernel; per 64-key tile each wave copies its two 2 KiB dS blocks
+// (32 keys x its 32 queries) into LDS and reads the B operand with transposing
+// reads.  In LDS the second 1 KiB half of a block (positions 16..31) sits 128
+// bytes further on, so the 32 lanes of a transposing read -- key rows
+// 16 (kk & 1) + 4 hi + 0..3 (and + 8) of both halves, 128 bytes each -- hit 64
+// distinct banks.  Column n of the result is the block's position n, i.e.
+// query ds_query_of(n) of the wave.  Blocks wholly above the diagonal were
+// never written; their MFMAs are skipped.
+// ---------------------------------------------------------------------------
+constexpr int kDsHalfElems = kDsBlockElems / 2;                // 1 KiB: 32 key rows x 16 positions
+constexpr int kDsHalfStride = kDsHalfElems + 64;               // + 128 bytes
+constexpr int kDsLdsBlockElems = 2 * kDsHalfStride;            // one block in LDS
+constexpr int kDsWaveElems = 2 * kDsLdsBlockElems;             // one wave's dS per 64-key tile
+
+__global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
+  constexpr int D = 128;
+  constexpr int DT = D / 32;
+  using L = TileLayout<D>;
+  static_assert(kBlockK == 2 * kDsBlock, "two dS blocks per key tile");
+  __shared__ __attribute__((aligned(16))) bf16_t sK0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sK1[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS0[kWaves * kDsWaveElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS1[kWaves * kDsWaveElems];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hi = lane >> 5;
+  const int rank = blockIdx.x / a.Hq;
+  const int h = blockIdx.x - rank * a.Hq;
+  const int2 item = a.plan[rank];
+  if (item.x < 0) return;  // list padding
+  const int s = item.x;
+  const int qtile = item.y;
+  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const int m0 = qtile * kBlockQ;
+  if (m0 >= g.nq) return;
+  const int hk = h / a.group;
+
+  const int wg_kend = max(g.p, min(m0 + kBlockQ, g.nq));
+  const int nkt = (wg_kend + kBlockK - 1) / kBlockK;
+  const int qa = m0 + wave * 32;
+  const bool wave_active = qa < g.nq;
+  const int w_kend_max = wave_active ? max(g.p, min(qa + 32, g.nq)) : 0;
+
+  const bf16_t* kseq = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
+  const TileLoader<D, kWaves> ldk(a.k_st, wave, lane);
+  // this wave's dS block row; reads past the row (or of a row outside the
+  // workspace) return zeros
+  const int row = g.start / kDsBlock + s + qa / kDsBlock;
+  const bool row_ok = wave_active && row < a.ds_rows;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(
+      a.dscore + ((int64_t)h * a.ds_rows + (row_ok ? row : 0)) * a.ds_width * kDsBlockElems,
+      row_ok ? (uint32_t)a.ds_width * kDsBlockElems * 2 : 0u);
+  const uint32_t s_voff = (uint32_t)lane * 16;
+
+  const bf16_t* i_k = kseq;
+  int i_rows = g.n;
+  int i_kt = 0;
+  auto issue_next = [&](bf16_t* tk, bf16_t* ts) {
+    ldk.issue_at(i_k, rows_bytes32(i_rows, (uint32_t)a.k_st, D), tk);
+    // the blocks this wave uses: key blocks 2 i_kt (+ 1) below w_kend_max
+    const int kb = i_kt * kBlockK;
+    bf16_t* const dst = ts + wave * kDsWaveElems;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+      if (kb + kDsBlock * mt < w_kend_max)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs, (__attribute__((address_space(3))) void*)(dst + mt * kDsLdsBlockElems + c * kDsHalfStride), 16,
+              s_voff,
+              (uint32_t)(2 * i_kt + mt) * (kDsBlockElems * 2) + c * 1024, 0, kNonTemporal);
+    i_k += kBlockK * a.k_st;
+    i_rows -= kBlockK;
+    ++i_kt;
+  };
+  issue_next(sK0, sS0);
+
+  f32x16 dqacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
+  const TileLanes<D> tl(lane);
+  // transposing-read lane offset inside a block: half (lane >> 4) & 1, key row
+  // 4 hi + (lane & 15) / 4, positions 4 (lane & 3) .. + 3 of the half
+  const int s_tr = ((lane >> 4) & 1) * kDsHalfStride + (4 * hi + ((lane & 15) >> 2)) * 16 + 4 * (lane & 3);
+
+  auto compute = [&](int kt, const bf16_t* sK, const bf16_t* sS) {
+    const int kb = kt * kBlockK;
+    if (!wave_active || kb >= w_kend_max) return;
+    const bf16_t* const sw = sS + wave * kDsWaveElems + s_tr;
+    const int nkk = kb + kDsBlock < w_kend_max ? 4 : 2;  // the second block may lie wholly above the diagonal
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk >= nkk) break;
+      const bf16_t* const bp = sw + (kk >> 1) * kDsLdsBlockElems + (kk & 1) * 16 * 16;
+      const bf16x8 sf = cat8(lds_read_tr16(bp), lds_read_tr16(bp + 8 * 16));
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16_t* kp = &sK[tl.tr_base + kk * 16 * L::kRowElems + dt * 32];
+        const bf16x4 k0 = lds_read_tr16(kp);
+        const bf16x4 k1 = lds_read_tr16(kp + L::kTrSecond);
+        dqacc[dt] = mfma32(cat8(k0, k1), sf, dqacc[dt]);
+      }
+    }
+  };
+
+  for (int kt = 0; kt < nkt; kt += 2) {
+    wait_vmem();
+    __syncthreads();
+    if (kt + 1 < nkt) issue_next(sK1, sS1);
+    compute(kt, sK0, sS0);
+    if (kt + 1 >= nkt) break;
+    wait_vmem();
+    __syncthreads();
+    if (kt + 2 < nkt) issue_next(sK0, sS0);
+    compute(kt + 1, sK1, sS1);
+  }
+
+  const int qpos = qa + ds_query_of(l32);
+  if (!wave_active || qpos >= g.nq) return;
+  bf16_t* drow = a.dq + (int64_t)(g.start + qpos) * a.dq_st + (int64_t)h * a.dq_sh;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      f32x4 t;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = dqacc[dt][4 * rg + e] * a.scale;
+      *(bf16x4*)&drow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_bwd_dq_ds_bf16(const BwdArgs& a, int numseqs, hipStream_t stream) {
+  static_assert(kBlockQ == kPlanTile, "work-list tiles are the dQ query tiles");
+  if (numseqs <= 0 || a.cap_q == 0) return hipSuccess;
+  // workgroup r * Hq + h: list entry r, head h
+  hipLaunchKernelGGL(dq_ds_kernel, dim3((unsigned)a.cap_q * (unsigned)a.Hq), dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace mimir

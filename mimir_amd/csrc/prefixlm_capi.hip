@@ -101,13 +101,22 @@ size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs,
   return (size_t)mimir::plan_capacity(total_tokens, numseqs, max_seqlen_all) * sizeof(int2);
 }
 
+size_t mimir_prefixlm_bwd_dscore_bytes(const MimirPrefixLMBwdParams* p) {
+  if (p == nullptr || p->dtype != MIMIR_DTYPE_BFLOAT16 || p->head_dim != 128 || p->total_tokens <= 0 ||
+      p->num_q_heads <= 0 || p->dscore_limit_bytes == 0)
+    return 0;
+  const mimir::DscoreGeom g = mimir::dscore_geometry(p->total_tokens, p->num_q_heads, p->numseqs, p->max_seqlen_all);
+  return g.bytes <= p->dscore_limit_bytes ? g.bytes : 0;
+}
+
 size_t mimir_prefixlm_bwd_workspace_size(const MimirPrefixLMBwdParams* p) {
   if (p == nullptr || p->total_tokens <= 0 || p->num_q_heads <= 0) return 0;
   const size_t dout_bytes = p->gate != nullptr ? (size_t)p->total_tokens * (size_t)p->num_q_heads *
                                                      (size_t)(p->head_dim > 0 ? p->head_dim : 0) *
                                                      (size_t)elem_bytes_of(p->dtype)
                                                : 0;
-  return mimir::bwd_workspace_layout(p->total_tokens, p->num_q_heads, p->numseqs, p->max_seqlen_all, dout_bytes)
+  return mimir::bwd_workspace_layout(p->total_tokens, p->num_q_heads, p->numseqs, p->max_seqlen_all, dout_bytes,
+                                     mimir_prefixlm_bwd_dscore_bytes(p))
       .total;
 }
 

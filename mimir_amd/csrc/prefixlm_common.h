@@ -326,11 +326,40 @@ constexpr int kSplitSlotFloats = 2 * 128 * 128;   // dK + dV partial of one part
 // Backward workspace sections (byte offsets, 256-byte aligned).
 // `dout_bytes`: the gated backward's upstream-gradient buffer (0 without a gate).
 struct BwdWorkspace {
-  size_t delta, lse2, plan_q, plan_k, counters, slots, dout, total;
+  size_t delta, lse2, plan_q, plan_k, counters, slots, dout, dscore, total;
   int cap_q, cap_k, pair_heads;
 };
 BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all,
-                                  size_t dout_bytes = 0);
+                                  size_t dout_bytes = 0, size_t dscore_bytes = 0);
+
+// Score-gradient hand-off from the dK / dV stage to the dQ stage: bf16 dS in
+// blocks of 32 queries x 32 keys (2 KiB), block index (h * rows + row) * width +
+// key / 32 with row = floor(start / 32) + s + query / 32 for sequence s starting
+// at packed token `start`.  Rows of consecutive sequences never overlap
+// (floor(start / 32) + ceil(n / 32) <= floor((start + n) / 32) + 1), so
+// rows = floor(T / 32) + numseqs + 1 and width = ceil(max_seqlen / 32) bound
+// every block of well-formed metadata.
+//
+// Inside a block the 32 queries sit at positions in the order the MFMA
+// accumulator of the dK / dV kernel leaves them -- position 16 a + 8 b + 4 c + e
+// is query 16 a + 8 c + 4 b + e (bits 2 and 3 swapped) -- and (key k, position
+// n) at byte (n / 16) * 1024 + k * 32 + (n % 16) * 2: two 1 KiB halves of
+// 32 key rows x 16 positions.
+constexpr int kDsBlock = 32;
+constexpr int kDsBlockElems = kDsBlock * kDsBlock;
+struct DscoreGeom {
+  int rows, width;
+  size_t bytes;
+};
+inline DscoreGeom dscore_geometry(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all) {
+  DscoreGeom g;
+  g.rows = total_tokens / kDsBlock + (numseqs > 0 ? numseqs : 0) + 1;
+  g.width = ((max_seqlen_all > 0 ? max_seqlen_all : 0) + kDsBlock - 1) / kDsBlock;
+  g.bytes = (size_t)(num_q_heads > 0 ? num_q_heads : 0) * (size_t)g.rows * (size_t)g.width * kDsBlockElems * 2;
+  return g;
+}
+// The position <-> query map of a block row (an involution).
+__host__ __device__ constexpr int ds_query_of(int pos) { return (pos & ~12) | ((pos & 4) << 1) | ((pos & 8) >> 1); }
 
 // delta[h, t] = sum_d O[t, h, d] * dO[t, h, d] and lse2[h, t] = lse[h, t] * log2(e), bf16 O / dO.
 // With a gate, `dout` is the gradient of the gated output: the rows also form

@@ -355,7 +355,7 @@ PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int nu
 }
 
 BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all,
-                                  size_t dout_bytes) {
+                                  size_t dout_bytes, size_t dscore_bytes) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   BwdWorkspace w;
   const size_t rows = (size_t)(total_tokens > 0 ? total_tokens : 0) * (size_t)(num_q_heads > 0 ? num_q_heads : 0);
@@ -371,6 +371,8 @@ BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs
   w.slots = align(w.counters + ((size_t)w.pair_heads + 2) * sizeof(int));
   w.dout = align(w.slots + (size_t)w.pair_heads * 2 * kSplitSlotFloats * sizeof(float));
   w.total = dout_bytes > 0 ? w.dout + dout_bytes : w.slots + (size_t)w.pair_heads * 2 * kSplitSlotFloats * sizeof(float);
+  w.dscore = align(w.total);
+  if (dscore_bytes > 0) w.total = w.dscore + dscore_bytes;
   return w;
 }
 

@@ -69,6 +69,24 @@ def set_validate_metadata(enabled: bool) -> None:
     _validate_metadata = bool(enabled)
 
 
+_dscore_limit_bytes = int(os.environ.get("MIMIR_PREFIXLM_DSCORE_LIMIT", str(4 << 30)))
+
+
+def set_dscore_workspace_limit(nbytes: int) -> None:
+    """Workspace bytes the backward may spend on stored score gradients.
+
+    With bf16 and head_dim 128 the dK / dV kernel can hand its bf16 dS tiles to
+    the dQ kernel, which then computes dQ = dS K without recomputing S and dP.
+    The tiles take ``Hq * (T / 32 + numseqs + 1) * ceil(max_seqlen / 32) * 2 KiB``
+    (about 1.1 GB for 8 x 2048 tokens and 16 heads); above this limit the dQ
+    kernel recomputes instead.  0 turns the hand-off off.  Default 4 GiB.
+    """
+    global _dscore_limit_bytes
+    if nbytes < 0:
+        raise ValueError("the limit is a byte count >= 0")
+    _dscore_limit_bytes = int(nbytes)
+
+
 def _scalar(x) -> int:
     return int(x.item()) if isinstance(x, Tensor) else int(x)
 
@@ -262,6 +280,7 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
     if gate is not None:
         p.gate, p.gate_stride_token, p.gate_stride_head = gate.data_ptr(), gate.stride(0), gate.stride(1)
         p.dgate, p.dgate_stride_token, p.dgate_stride_head = dgate.data_ptr(), dgate.stride(0), dgate.stride(1)
+    p.dscore_limit_bytes = _dscore_limit_bytes
     ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p)))
     ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
     p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes

@@ -147,6 +147,29 @@ def test_validation_errors_map_to_reference_exceptions(lib):
     assert rc == _capi.ERR_INVALID_ARGUMENT and b"q is NULL" in lib.mimir_prefixlm_last_error()
 
 
+def test_dscore_workspace_bytes(lib):
+    """The score-gradient hand-off: Hq x (T/32 + numseqs + 1) x ceil(max_seqlen/32) blocks of
+    2 KiB, only for bf16 with head_dim 128 and only within dscore_limit_bytes; the workspace
+    grows by exactly that (after 256-byte alignment)."""
+    p = _capi.BwdParams()
+    p.total_tokens, p.num_q_heads, p.num_kv_heads, p.numseqs, p.max_seqlen_all = 1000, 8, 2, 3, 700
+    p.head_dim, p.dtype = 128, _capi.DTYPE_BFLOAT16
+    expect = 8 * (1000 // 32 + 3 + 1) * ((700 + 31) // 32) * 2048
+    p.dscore_limit_bytes = 0
+    assert lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)) == 0
+    base = lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p))
+    assert base == lib.mimir_prefixlm_bwd_workspace_bytes(1000, 8, 3, 700)
+    for limit, got in ((expect - 1, 0), (expect, expect), (1 << 40, expect)):
+        p.dscore_limit_bytes = limit
+        assert lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)) == got
+        size = lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p))
+        assert size == (base if got == 0 else ((base + 255) // 256) * 256 + expect)
+    p.head_dim = 64
+    assert lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)) == 0
+    p.head_dim, p.dtype = 128, _capi.DTYPE_FLOAT32
+    assert lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)) == 0
+
+
 def test_unknown_backward_stage_bits(lib):
     p = _capi.BwdParams()
     assert lib.mimir_prefixlm_bwd_stages(ctypes.byref(p), 64, None) == _capi.ERR_INVALID_ARGUMENT

@@ -127,6 +127,45 @@ def test_bf16_random_shapes(device, seed):
     check(case, device, label=f"random{seed} hq={hq} hkv={hkv} d={d} causal={causal} pad={pad_to}")
 
 
+@pytest.fixture
+def dscore_limit():
+    """Set the score-gradient workspace limit for one test; the default comes back after."""
+    from mimir_amd import prefixlm as P
+
+    saved = P._dscore_limit_bytes
+    yield P.set_dscore_workspace_limit
+    P.set_dscore_workspace_limit(saved)
+
+
+@pytest.mark.parametrize("idx", [1, 3, 4, 8])
+def test_bf16_recompute_dq(device, idx, dscore_limit):
+    """The dQ kernel that recomputes S and dP (score-gradient hand-off off) meets the same bar."""
+    dscore_limit(0)
+    seq_lens, prefixes, hq, hkv, d, pad_to, causal = SMALL[idx]
+    case = make_case(seq_lens, prefixes, hq, hkv, d, seed=idx, dtype=torch.bfloat16, pad_to=pad_to,
+                     is_causal=causal)
+    check(case, device, label=f"recompute small{idx}")
+
+
+def test_dscore_handoff_matches_recompute(device, dscore_limit):
+    """dK / dV are bitwise the same with and without the hand-off (the stores change no
+    arithmetic); dQ from the stored dS agrees with the recomputed one to bf16 rounding of dS; a
+    limit below the tiles' size falls back to the recompute, bit for bit."""
+    case = make_case([900, 333, 64, 5], [450, 0, 64, 2], 8, 2, 128, seed=21, dtype=torch.bfloat16, pad_to=1400)
+    dscore_limit(4 << 30)
+    on = run_gpu(case, device)
+    dscore_limit(0)
+    off = run_gpu(case, device)
+    dscore_limit(1)
+    tiny = run_gpu(case, device)
+    assert torch.equal(on["dk"], off["dk"]) and torch.equal(on["dv"], off["dv"])
+    err = (on["dq"] - off["dq"]).abs().max().item()
+    print(f"[parity] dscore hand-off vs recompute: dq max diff {err:.3g}", flush=True)
+    assert err <= 1e-2
+    for key in ("dq", "dk", "dv"):
+        assert torch.equal(tiny[key], off[key])
+
+
 @pytest.mark.parametrize("idx", [0, 1, 2, 4, 5, 6, 8])
 def test_f32_small(device, idx):
     seq_lens, prefixes, hq, hkv, d, pad_to, causal = SMALL[idx]
