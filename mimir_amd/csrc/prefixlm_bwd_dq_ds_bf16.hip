@@ -16,9 +16,11 @@ constexpr int kNonTemporal = 2;  // buffer cache policy: streaming (nt), for dS 
 // dQ from the stored score gradients (head_dim 128): dQ^T += K^T dS^T with dS
 // read from the blocks the dK / dV kernel wrote (dscore_geometry in
 // prefixlm_common.h) instead of recomputed.  Same owner, work list and K tiles
-// as dq_kernel; per 64-key tile each wave copies its two 2 KiB dS blocks
-// (32 keys x its 32 queries) into LDS and reads the B operand with transposing
-// reads.  In LDS the second 1 KiB half of a block (positions 16..31) sits 128
+// as dq_kernel (two K stages shared by the workgroup); per 64-key tile each
+// wave copies its two 2 KiB dS blocks (32 keys x its 32 queries) into its own
+// LDS region -- one region per wave, refilled as soon as the wave's MFMAs have
+// consumed it, which keeps the workgroup at 52 KiB of LDS and three workgroups
+// per CU streaming dS -- and reads the B operand with transposing reads.  In LDS the second 1 KiB half of a block (positions 16..31) sits 128
 // bytes further on, so the 32 lanes of a transposing read -- key rows
 // 16 (kk & 1) + 4 hi + 0..3 (and + 8) of both halves, 128 bytes each -- hit 64
 // distinct banks.  Column n of the result is the block's position n, i.e.
@@ -37,8 +39,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
   static_assert(kBlockK == 2 * kDsBlock, "two dS blocks per key tile");
   __shared__ __attribute__((aligned(16))) bf16_t sK0[L::kElems];
   __shared__ __attribute__((aligned(16))) bf16_t sK1[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sS0[kWaves * kDsWaveElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sS1[kWaves * kDsWaveElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS[kWaves * kDsWaveElems];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -76,11 +77,17 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
   const bf16_t* i_k = kseq;
   int i_rows = g.n;
   int i_kt = 0;
-  auto issue_next = [&](bf16_t* tk, bf16_t* ts) {
+  auto issue_k = [&](bf16_t* tk) {
     ldk.issue_at(i_k, rows_bytes32(i_rows, (uint32_t)a.k_st, D), tk);
+    i_k += kBlockK * a.k_st;
+    i_rows -= kBlockK;
+  };
+  // dS of key tile i_kt into this wave's own LDS region (no workgroup barrier:
+  // only this wave reads it)
+  auto issue_ds = [&]() {
     // the blocks this wave uses: key blocks 2 i_kt (+ 1) below w_kend_max
     const int kb = i_kt * kBlockK;
-    bf16_t* const dst = ts + wave * kDsWaveElems;
+    bf16_t* const dst = sS + wave * kDsWaveElems;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
       if (kb + kDsBlock * mt < w_kend_max)
@@ -90,11 +97,10 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
               rs, (__attribute__((address_space(3))) void*)(dst + mt * kDsLdsBlockElems + c * kDsHalfStride), 16,
               s_voff,
               (uint32_t)(2 * i_kt + mt) * (kDsBlockElems * 2) + c * 1024, 0, kNonTemporal);
-    i_k += kBlockK * a.k_st;
-    i_rows -= kBlockK;
     ++i_kt;
   };
-  issue_next(sK0, sS0);
+  issue_k(sK0);
+  issue_ds();
 
   f32x16 dqacc[DT];
 #pragma unroll
@@ -104,7 +110,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
   // 4 hi + (lane & 15) / 4, positions 4 (lane & 3) .. + 3 of the half
   const int s_tr = ((lane >> 4) & 1) * kDsHalfStride + (4 * hi + ((lane & 15) >> 2)) * 16 + 4 * (lane & 3);
 
-  auto compute = [&](int kt, const bf16_t* sK, const bf16_t* sS) {
+  auto compute = [&](int kt, const bf16_t* sK) {
     const int kb = kt * kBlockK;
     if (!wave_active || kb >= w_kend_max) return;
     const bf16_t* const sw = sS + wave * kDsWaveElems + s_tr;
@@ -124,16 +130,26 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
     }
   };
 
+  // The wave's dS reads of tile kt are complete (their MFMAs consumed them)
+  // before its copy of tile kt + 1 into the same region is issued.
+  auto next_ds = [&](int kt) {
+    if (kt + 1 >= nkt) return;
+    wait_lds();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_ds();
+  };
   for (int kt = 0; kt < nkt; kt += 2) {
     wait_vmem();
     __syncthreads();
-    if (kt + 1 < nkt) issue_next(sK1, sS1);
-    compute(kt, sK0, sS0);
+    if (kt + 1 < nkt) issue_k(sK1);
+    compute(kt, sK0);
+    next_ds(kt);
     if (kt + 1 >= nkt) break;
     wait_vmem();
     __syncthreads();
-    if (kt + 2 < nkt) issue_next(sK0, sS0);
-    compute(kt + 1, sK1, sS1);
+    if (kt + 2 < nkt) issue_k(sK0);
+    compute(kt + 1, sK1);
+    next_ds(kt + 1);
   }
 
   const int qpos = qa + ds_query_of(l32);
