@@ -250,38 +250,55 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
     step(kt + 1, sK1, sV1);
   }
 
+  // Epilogue: each wave stages its 32 output rows (and the gated rows) in LDS --
+  // one K / V stage object per wave, free once every wave is past the tile
+  // loop -- and stores whole rows, kRowsPerInst rows of D * 2 contiguous bytes
+  // per store instruction instead of 32 pieces of 16 bytes.
+  __syncthreads();
   if (!wave_active) return;
   const float l_tot = xor32_sum(l_run);
   const float inv = 1.f / l_tot;
-  if (qpos < g.nq) {
-    bf16_t* orow = a.o + (int64_t)(g.start + qpos) * a.o_st + (int64_t)h * a.o_sh;
+  constexpr int kPitch = D + 8;                 // elements; rows stay 16-byte aligned
+  constexpr int kUnits = D / 8;                 // 16-byte units per row
+  constexpr int kRowsPerInst = 64 / kUnits;
+  static_assert((kGated ? 2 : 1) * 32 * kPitch <= L::kElems, "a wave's rows fit its stage object");
+  bf16_t* const stage = wave == 0 ? sK0 : wave == 1 ? sV0 : wave == 2 ? sK1 : sV1;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        f32x4 t;
+    for (int rg = 0; rg < 4; ++rg) {
+      f32x4 t;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = oacc[dt][4 * rg + e] * inv;
-        *(bf16x4*)&orow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
+      for (int e = 0; e < 4; ++e) t[e] = oacc[dt][4 * rg + e] * inv;
+      *(bf16x4*)&stage[l32 * kPitch + 32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
+      if constexpr (kGated != 0) {
+        // Sigmoid output gate in the store (layers.py:239): y = round(s * O) with
+        // s = round(sigmoid(gate)) and O the rounded attention output, as the
+        // reference's bf16 torch.sigmoid(gate) * attn_output rounds them.
+        f32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (float)sgate[4 * dt + rg][e] * round_to(t[e], bf16_t());
+        *(bf16x4*)&stage[(32 + l32) * kPitch + 32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(y, bf16x4);
       }
-    if constexpr (kGated != 0) {
-      // Sigmoid output gate in the store (layers.py:239): y = round(s * O) with
-      // s = round(sigmoid(gate)) and O the rounded attention output, as the
-      // reference's bf16 torch.sigmoid(gate) * attn_output rounds them.
-      bf16_t* yrow = a.y + (int64_t)(g.start + qpos) * a.y_st + (int64_t)h * a.y_sh;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
-          f32x4 t;
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            t[e] = (float)sgate[4 * dt + rg][e] * round_to(oacc[dt][4 * rg + e] * inv, bf16_t());
-          *(bf16x4*)&yrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
-        }
     }
-    if (hi == 0 && a.lse != nullptr)
-      a.lse[(int64_t)h * a.lse_sh + g.start + qpos] = m_run * a.scale + fast_log2(l_tot) * kLn2;
+  if (hi == 0 && a.lse != nullptr && qpos < g.nq)
+    a.lse[(int64_t)h * a.lse_sh + g.start + qpos] = m_run * a.scale + fast_log2(l_tot) * kLn2;
+  // The LDS unit runs one wave's accesses in order: the reads below see the writes above.
+  __asm__ volatile("" ::: "memory");
+  const int u = lane % kUnits;
+  bf16_t* const obase = a.o + (int64_t)(g.start + qa) * a.o_st + (int64_t)h * a.o_sh + u * 8;
+  bf16_t* ybase = nullptr;
+  if constexpr (kGated != 0) ybase = a.y + (int64_t)(g.start + qa) * a.y_st + (int64_t)h * a.y_sh + u * 8;
+#pragma unroll
+  for (int j = 0; j < 32 / kRowsPerInst; ++j) {
+    const int r = j * kRowsPerInst + lane / kUnits;
+    const bf16x8 ov = *(const bf16x8*)&stage[r * kPitch + u * 8];
+    bf16x8 yv;
+    if constexpr (kGated != 0) yv = *(const bf16x8*)&stage[(32 + r) * kPitch + u * 8];
+    if (qa + r < g.nq) {
+      *(bf16x8*)&obase[(int64_t)r * a.o_st] = ov;
+      if constexpr (kGated != 0) *(bf16x8*)&ybase[(int64_t)r * a.y_st] = yv;
+    }
   }
 }
 
