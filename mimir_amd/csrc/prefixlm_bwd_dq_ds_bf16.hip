@@ -152,9 +152,17 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
     next_ds(kt + 1);
   }
 
-  const int qpos = qa + ds_query_of(l32);
-  if (!wave_active || qpos >= g.nq) return;
-  bf16_t* drow = a.dq + (int64_t)(g.start + qpos) * a.dq_st + (int64_t)h * a.dq_sh;
+  // Epilogue: the wave stages its 32 dQ rows in LDS (half of a K stage object,
+  // free once every wave is past the tile loop), in query order, and stores
+  // whole rows: kRowsPerInst rows of D * 2 contiguous bytes per instruction.
+  __syncthreads();
+  if (!wave_active) return;
+  constexpr int kPitch = D + 8;  // elements; rows stay 16-byte aligned
+  constexpr int kUnits = D / 8;  // 16-byte units per row
+  constexpr int kRowsPerInst = 64 / kUnits;
+  static_assert(2 * 32 * kPitch <= L::kElems, "two waves' rows fit one K stage object");
+  bf16_t* const stage = (wave < 2 ? sK0 : sK1) + (wave & 1) * 32 * kPitch;
+  const int srow = ds_query_of(l32);
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -162,8 +170,18 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
       f32x4 t;
 #pragma unroll
       for (int e = 0; e < 4; ++e) t[e] = dqacc[dt][4 * rg + e] * a.scale;
-      *(bf16x4*)&drow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
+      *(bf16x4*)&stage[srow * kPitch + 32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
     }
+  // The LDS unit runs one wave's accesses in order: the reads below see the writes above.
+  __asm__ volatile("" ::: "memory");
+  const int u = lane % kUnits;
+  bf16_t* const dbase = a.dq + (int64_t)(g.start + qa) * a.dq_st + (int64_t)h * a.dq_sh + u * 8;
+#pragma unroll
+  for (int j = 0; j < 32 / kRowsPerInst; ++j) {
+    const int r = j * kRowsPerInst + lane / kUnits;
+    const bf16x8 v = *(const bf16x8*)&stage[r * kPitch + u * 8];
+    if (qa + r < g.nq) *(bf16x8*)&dbase[(int64_t)r * a.dq_st] = v;
+  }
 }
 
 }  // namespace
