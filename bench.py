@@ -12,7 +12,10 @@ padding fill), all through the C ABI on torch's current stream.  The default wor
 FLOPs with N = sum over sequences of (n^2 + n + p^2 - p)/2.  The roofline entry
 is for the kernel that takes the most time; its algorithmic FLOPs per launch are
 fwd 4*D*Hq*N, dK/dV 8*D*Hq*N (S recompute, dP, dV, dK) and dQ 2*D*Hq*N (dQ only;
-its S/dP recompute is not counted), so the three add up to the step's 14*D*Hq*N.
+when dQ recomputes S and dP, that is not counted), so the three add up to the
+step's 14*D*Hq*N.  With the score-gradient hand-off (bf16, head_dim 128) the dQ
+kernel reads the dS blocks the dK/dV kernel stored; the line then also gives its
+streamed bytes and bandwidth (``dq_ds_bytes``, ``dq_ds_gbs``).
 Kernel durations come from a second pass of K steps with the stages serialized
 (``mimir_prefixlm_bwd_stages``) and HIP events recorded on the launch stream
 between them.  The CPU baseline times the oracle's restatement of the reference
