@@ -526,6 +526,11 @@ def main() -> int:
     if measured is not None:
         res["roofline"]["traffic"] = measured["bytes"]
         res["roofline"]["traffic_source"] = measured["source"]
+        # the same kernel's measured HBM traffic over its duration: how close it also is to the
+        # HBM bound (with the dS hand-off the dK/dV kernel streams 0.7 GB of dS out)
+        gbs = measured["bytes"] / (stage_avg[dom] * 1e-3) / 1e9
+        res["roofline"]["traffic_gbs"] = round(gbs, 1)
+        res["roofline"]["traffic_frac_of_hbm"] = round(gbs / HBM_GBS, 4)
     if not fwd_only:
         res["bwd_tflops"] = round(f_bwd / ((ms_per_step - stage_avg["fwd"]) * 1e-3) / 1e12, 2)
     res["dscore_handoff"] = handoff
