@@ -247,3 +247,50 @@ def test_backward_matches_its_stages(device):
         grads.append((dq.clone(), dk.clone(), dv.clone()))
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_graph_replay_matches_eager(device, d):
+    """Forward + backward captured in a HIP graph: every replay, with eager calls between them,
+    gives bitwise the eager result (the work lists, split counters and work queue are rebuilt or
+    reset by the launches themselves; no memset nodes)."""
+    import ctypes
+
+    from mimir_amd import _capi
+    from mimir_amd import prefixlm as P
+
+    case = make_case([700, 300, 45], [350, 0, 45], 8, 2, d, seed=12, dtype=torch.bfloat16, pad_to=1100)
+    c = case.to(device)
+    lib = _capi.load()
+    scale = 1.0 / d ** 0.5
+    fp, out, lse, _kf = P.prepare_fwd(c.q, c.k, c.v, False, c.prefix_lens, c.causal_lens, c.cu_seqlens,
+                                      c.total_seqlen, c.numseqs, c.max_seqlen_all, scale)
+    bp, dq, dk, dv, _kb = P.prepare_bwd(c.dout, c.q, c.k, c.v, out, lse, False, c.prefix_lens, c.causal_lens,
+                                        c.cu_seqlens, c.total_seqlen, c.numseqs, c.max_seqlen_all, scale)
+
+    def step():
+        stream = torch.cuda.current_stream(device).cuda_stream
+        _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(fp), stream))
+        _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd(ctypes.byref(bp), stream))
+
+    step()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in (out, lse, dq, dk, dv)]
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        step()  # warm-up on the capture stream
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, ref in zip((out, lse, dq, dk, dv), eager):
+            assert torch.equal(got, ref)
+        step()
+        torch.cuda.synchronize()
+        for got, ref in zip((out, lse, dq, dk, dv), eager):
+            assert torch.equal(got, ref)
