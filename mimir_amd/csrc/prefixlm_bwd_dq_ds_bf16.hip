@@ -10,7 +10,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kBlockQ = 128;  // query rows per workgroup (32 per wave)
 constexpr int kBlockK = 64;   // keys per LDS tile
-constexpr int kNonTemporal = 2;  // buffer cache policy: streaming (nt), for dS read once
+constexpr int kNonTemporal = 2;  // buffer cache policy: streaming (nt); dS is read once
 
 // ---------------------------------------------------------------------------
 // dQ from the stored score gradients (head_dim 128): dQ^T += K^T dS^T with dS
@@ -20,17 +20,18 @@ constexpr int kNonTemporal = 2;  // buffer cache policy: streaming (nt), for dS 
 // wave copies its two 2 KiB dS blocks (32 keys x its 32 queries) into its own
 // LDS region -- one region per wave, refilled as soon as the wave's MFMAs have
 // consumed it, which keeps the workgroup at 52 KiB of LDS and three workgroups
-// per CU streaming dS -- and reads the B operand with transposing reads.  In LDS the second 1 KiB half of a block (positions 16..31) sits 128
-// bytes further on, so the 32 lanes of a transposing read -- key rows
+// per CU streaming dS -- and reads the B operand with transposing reads.  In
+// LDS the second 1 KiB half of a block (positions 16..31) sits 128 bytes
+// further on, so the 32 lanes of a transposing read -- key rows
 // 16 (kk & 1) + 4 hi + 0..3 (and + 8) of both halves, 128 bytes each -- hit 64
 // distinct banks.  Column n of the result is the block's position n, i.e.
 // query ds_query_of(n) of the wave.  Blocks wholly above the diagonal were
-// never written; their MFMAs are skipped.
+// never written; their loads and MFMAs are skipped.
 // ---------------------------------------------------------------------------
-constexpr int kDsHalfElems = kDsBlockElems / 2;                // 1 KiB: 32 key rows x 16 positions
-constexpr int kDsHalfStride = kDsHalfElems + 64;               // + 128 bytes
-constexpr int kDsLdsBlockElems = 2 * kDsHalfStride;            // one block in LDS
-constexpr int kDsWaveElems = 2 * kDsLdsBlockElems;             // one wave's dS per 64-key tile
+constexpr int kDsHalfElems = kDsBlockElems / 2;      // 1 KiB: 32 key rows x 16 positions
+constexpr int kDsHalfStride = kDsHalfElems + 64;     // + 128 bytes
+constexpr int kDsLdsBlockElems = 2 * kDsHalfStride;  // one block in LDS
+constexpr int kDsWaveElems = 2 * kDsLdsBlockElems;   // one wave's dS per 64-key tile
 
 __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
   constexpr int D = 128;
