@@ -1,7 +1,7 @@
 // bf16 prefix-LM attention backward, dK / dV kernel for head_dim 128 with two
 // waves per SIMD, for gfx950 (MI355X).  Owner = (kv head, 128-key tile), the
-// same split and grid as the one-wave-per-SIMD kernel in
-// prefixlm_bwd_dkdv_bf16.hip, and the same math:
+// same work list as the head_dim 64 kernel in prefixlm_bwd_dkdv_bf16.hip, and
+// the same math:
 //   per q head of the GQA group and 64-query tile:
 //     S = Q K^T, dP = dO V^T, P = exp2(S * scale * log2 e - lse2),
 //     dS = P (dP - delta), dV^T += dO^T P, dK^T += Q^T dS.
@@ -247,10 +247,10 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     bf16x8 pb[2], db[2];
     // dS half s2 (positions 16 s2 .. + 15 of the block: 1 KiB of 32 key rows
     // of 32 bytes) to key row l32, positions 16 s2 + 8 hi + 0..7: one store
-    // instruction writes 1 KiB contiguously, non-temporal (cache policy nt), so
-    // the stream of dS does not push the Q / dO tiles other workgroups reuse out
-    // of L2.  The stores join the vmcnt queue behind the tile copies in flight,
-    // so the stage waits stay conservative.
+    // instruction writes 1 KiB contiguously, non-temporal (cache policy nt):
+    // nothing reads the blocks again before the dQ kernel.  The stores join the
+    // vmcnt queue behind the tile copies in flight, so the stage waits stay
+    // conservative.
     __amdgpu_buffer_rsrc_t rds;
     if constexpr (kStoreDs) {
       const int row = ds_row0 + (qr >> 5);
