@@ -49,15 +49,17 @@ def _cores() -> int:
     return max(1, n)
 
 
-def cpu_baseline(case, target_seconds: float = 12.0, unit_bytes_cap: float = 3e9) -> dict:
-    """Oracle masked-SDPA fwd+bwd (fp32, autograd) over a bounded sample of the batch.
+def cpu_baseline(case, target_seconds: float = 4.0, unit_bytes_cap: float = 3e9, runs: int = 3) -> dict:
+    """Oracle masked-SDPA fwd+bwd and fwd alone (fp32, autograd) over a bounded sample of the batch.
 
-    The sample is a round-robin over units = (sequence, range of q-heads), each
-    run densely as its own packed batch, until about ``target_seconds`` of CPU
-    time have been spent (after one untimed warm-up unit).  A unit holds as many
-    whole kv-head groups as fit in ``unit_bytes_cap`` of fp32 score matrices, or
-    fewer q-heads of one group when a single group does not fit.  FLOPs count
-    the unit's attended pairs only, like the GPU figure.
+    The sample is a fixed round-robin list of units = (sequence, range of q-heads),
+    each run densely as its own packed batch: as many units as one fwd+bwd pass
+    covers in about ``target_seconds`` (after one untimed warm-up unit).  A unit
+    holds as many whole kv-head groups as fit in ``unit_bytes_cap`` of fp32 score
+    matrices, or fewer q-heads of one group when a single group does not fit.
+    The sample is then timed ``runs`` times fwd+bwd and ``runs`` times forward
+    only; the medians are reported.  FLOPs count the units' attended pairs
+    only, like the GPU figure.
     """
     import torch
 
@@ -87,36 +89,53 @@ def cpu_baseline(case, target_seconds: float = 12.0, unit_bytes_cap: float = 3e9
                 case.v[sl, kv0:kv0 + kvw].float().contiguous(), case.dout[sl, q0:q0 + qw].float().contiguous())
         return build_case(tens, [n], [p], is_causal=case.is_causal)
 
-    def run(sample):
-        q, k, v = (t.clone().requires_grad_(True) for t in (sample.q, sample.k, sample.v))
-        o = dense_forward_autograd(q, k, v, sample.is_causal, *sample.oracle_args())
-        o.backward(sample.dout)
+    def run(sample, backward=True):
+        q, k, v = (t.clone().requires_grad_(backward) for t in (sample.q, sample.k, sample.v))
+        if backward:
+            dense_forward_autograd(q, k, v, sample.is_causal, *sample.oracle_args()).backward(sample.dout)
+        else:
+            with torch.no_grad():
+                dense_forward_autograd(q, k, v, sample.is_causal, *sample.oracle_args())
 
     run(make(units[0]))  # warm-up
-    flops = 0.0
+    chosen = []  # the sample: units until one fwd+bwd pass takes target_seconds
     elapsed = 0.0
-    done = 0
     while elapsed < target_seconds:
-        sample = make(units[done % len(units)])
+        sample = make(units[len(chosen) % len(units)])
         t0 = time.perf_counter()
         run(sample)
         elapsed += time.perf_counter() - t0
-        flops += sample.fwd_flops() + sample.bwd_flops()
-        done += 1
+        chosen.append(sample)
+    flops_fwd = sum(s.fwd_flops() for s in chosen)
+    flops = flops_fwd + sum(s.bwd_flops() for s in chosen)
+
+    def timed(backward):
+        t0 = time.perf_counter()
+        for smp in chosen:
+            run(smp, backward)
+        return time.perf_counter() - t0
+
+    t_step = statistics.median(timed(True) for _ in range(runs))
+    t_fwd = statistics.median(timed(False) for _ in range(runs))
+    done = len(chosen)
     try:
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except Exception:  # noqa: BLE001
         model = "unknown"
     widths = sorted({u[2] for u in units})
     return {
-        "value": round(flops / elapsed / 1e12, 5),
+        "value": round(flops / t_step / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
         "sample": (f"{done} units of (sequence, {'/'.join(map(str, widths))} q-heads) of the "
                    f"same batch ({len(units)} units cover it; round-robin from sequence 0), each fwd+bwd as fp32 "
-                   f"torch SDPA with a bool prefix-LM mask + autograd; {elapsed:.1f} s timed after 1 warm-up unit"),
-        "seconds": round(elapsed, 3),
+                   f"torch SDPA with a bool prefix-LM mask + autograd; median of {runs} timed passes over the "
+                   f"sample after 1 warm-up unit"),
+        "seconds": round(t_step, 3),
+        "fwd_value": round(flops_fwd / t_fwd / 1e12, 5),
+        "fwd_seconds": round(t_fwd, 3),
+        "runs": runs,
         "cpu_model": model,
         "torch": torch.__version__,
     }
@@ -362,7 +381,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5, 6])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layer", action="store_true",
@@ -373,6 +392,10 @@ def main() -> int:
                     help="instead of the operator, time KV-cache attention (inference): decode (S = 1) and a "
                          "prefill chunk into a filled cache, fused (mimir_amd.cache) against the reference's "
                          "torch composition")
+    ap.add_argument("--autograd", action="store_true",
+                    help="time the drop-in as Mimir2 calls it: flash_attn_varlen_prefixlm through autograd "
+                         "(custom ops, argument checks, allocation of outputs and workspaces) and .backward(), "
+                         "instead of replaying prepared C-ABI calls")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="instead of the step, time a plain device copy of this many MiB (reference kernel of known "
                          "HBM traffic for scaling the FETCH_SIZE / WRITE_SIZE counters)")
@@ -408,12 +431,18 @@ def main() -> int:
     lib = _capi.load()
     stream = torch.cuda.current_stream(dev).cuda_stream
 
+    # as the autograd path runs it: for bf16 the forward records its split decision
+    # (split mode AUTO) and writes the low output half when it splits; the backward
+    # follows that decision and reads the low half for its delta rows then
+    out_lo = torch.empty_like(c.q) if elem == 2 else None
+    flag = torch.empty(1 if elem == 2 else 0, dtype=torch.int32, device=dev)
     fp, out, lse, keep_f = P.prepare_fwd(c.q, c.k, c.v, case.is_causal, c.prefix_lens, c.causal_lens, c.cu_seqlens,
-                                         c.total_seqlen, c.numseqs, c.max_seqlen_all, scale)
+                                         c.total_seqlen, c.numseqs, c.max_seqlen_all, scale, out_lo=out_lo,
+                                         split_flag=flag)
     _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(fp), stream))
     bp, dq, dk, dv, keep_b = P.prepare_bwd(c.dout, c.q, c.k, c.v, out, lse, case.is_causal, c.prefix_lens,
                                            c.causal_lens, c.cu_seqlens, c.total_seqlen, c.numseqs,
-                                           c.max_seqlen_all, scale)
+                                           c.max_seqlen_all, scale, out_lo=out_lo, split_flag=flag)
     fwd_only = args.workload == 1
     stages = [("fwd", None)]
     if not fwd_only:
@@ -424,13 +453,40 @@ def main() -> int:
 
     bwd_fn = lib.mimir_prefixlm_bwd
 
-    def step():
-        """One operator step as the autograd path runs it: forward, then the whole backward."""
-        rc = fwd_fn(fpr, stream)
-        if rc == 0 and not fwd_only:
+    if args.autograd:
+        from mimir_amd import flash_attn_varlen_prefixlm
+
+        qg, kg, vg = (t.detach().clone().requires_grad_(not fwd_only) for t in (c.q, c.k, c.v))
+        call_args = (c.prefix_lens, c.causal_lens, c.cu_seqlens, c.total_seqlen, c.numseqs, c.max_seqlen_prefix,
+                     c.max_seqlen_causal, c.max_seqlen_all)
+
+        def run_fwd():
+            return flash_attn_varlen_prefixlm(qg, kg, vg, case.is_causal, *call_args)
+
+        def run_bwd(o):
+            o.backward(c.dout)
+
+        def step():
+            """flash_attn_varlen_prefixlm + .backward(): host checks, allocations and launches included."""
+            o = run_fwd()
+            if not fwd_only:
+                run_bwd(o)
+    else:
+        def run_fwd():
+            rc = fwd_fn(fpr, stream)
+            if rc:
+                _capi.raise_for_status(lib, rc)
+
+        def run_bwd(_):
             rc = bwd_fn(bpr, stream)
-        if rc:
-            _capi.raise_for_status(lib, rc)
+            if rc:
+                _capi.raise_for_status(lib, rc)
+
+        def step():
+            """One operator step as the autograd path runs it: forward, then the whole backward."""
+            o = run_fwd()
+            if not fwd_only:
+                run_bwd(o)
 
     def staged_step(evs):
         """The same work one stage at a time, with HIP events between the stages."""
@@ -460,6 +516,19 @@ def main() -> int:
     total_ms = t_start.elapsed_time(t_end)
     ms_per_step = total_ms / K
 
+    # Forward and forward + backward per step, HIP events on the launch stream: medians of K runs.
+    pe = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    for k in range(K):
+        pe[k][0].record()
+        o = run_fwd()
+        pe[k][1].record()
+        if not fwd_only:
+            run_bwd(o)
+        pe[k][2].record()
+    torch.cuda.synchronize()
+    fwd_med = statistics.median(e[0].elapsed_time(e[1]) for e in pe)
+    step_med = statistics.median(e[0].elapsed_time(e[2]) for e in pe)
+
     # Per-kernel durations: K more steps with the stages serialized and bracketed by events.
     for k in range(K):
         staged_step(evs[k])
@@ -467,7 +536,7 @@ def main() -> int:
     stage_ms = {name: [evs[k][i].elapsed_time(evs[k][i + 1]) for k in range(K)] for i, (name, _) in enumerate(stages)}
     stage_avg = {name: sum(v) / len(v) for name, v in stage_ms.items()}
     stage_med = {name: statistics.median(v) for name, v in stage_ms.items()}
-    step_med = statistics.median(sum(stage_ms[n][k] for n, _ in stages) for k in range(K))
+    staged_med = statistics.median(sum(stage_ms[n][k] for n, _ in stages) for k in range(K))
 
     pairs = case.pairs()
     f_fwd = 4.0 * d * hq * pairs
@@ -477,6 +546,10 @@ def main() -> int:
     peak = PEAK_F32_TFLOPS if c.q.dtype == torch.float32 else PEAK_BF16_TFLOPS
     kernel_flops = {"fwd": f_fwd, "dkdv": 8.0 * d * hq * pairs, "dq": 2.0 * d * hq * pairs}
     handoff = not fwd_only and int(lib.mimir_prefixlm_bwd_dscore_bytes(bpr)) > 0  # dQ reads dK/dV's dS
+    # the device-side AUTO rule (softmax_scale * max|K| > 0.75) on the host copy of K: with the split
+    # the recomputing dQ does the work even where the hand-off region exists
+    split = elem == 2 and not fwd_only and bool(case.k.float().abs().max().item() * scale > 0.75)
+    handoff = handoff and not split
     kernel_names = {"fwd": "fwd_bf16_kernel" if elem == 2 else "fwd_f32_kernel",
                     "dkdv": ("dkdv_pair_ds_kernel" if handoff else "dkdv_pair_kernel") if (elem == 2 and d == 128)
                     else "dkdv_kernel",
@@ -504,10 +577,16 @@ def main() -> int:
             "q_heads": hq, "kv_heads": hkv, "head_dim": d, "seed": args.seed,
             "attended_pairs": pairs, "passes": "fwd" if fwd_only else "fwd+bwd",
             "parallelism": "single-gpu",
+            "path": ("flash_attn_varlen_prefixlm + autograd backward (host work included)" if args.autograd
+                     else "C-ABI mimir_prefixlm_fwd + mimir_prefixlm_bwd, prepared parameter structs"),
         },
         "pct_of_peak": round(100.0 * value / peak, 2),
         "hbm_gbs_algorithmic": round(alg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
-        "staged_step_ms_median": round(step_med, 5),
+        "fwd_ms_median": round(fwd_med, 5),
+        "step_ms_median": round(step_med, 5),
+        "fwd_tflops_median": round(f_fwd / (fwd_med * 1e-3) / 1e12, 2),
+        "step_tflops_median": round(flops / (step_med * 1e-3) / 1e12, 2),
+        "staged_step_ms_median": round(staged_med, 5),
         "stage_ms_avg": {n: round(v, 5) for n, v in stage_avg.items()},
         "stage_ms_median": {n: round(v, 5) for n, v in stage_med.items()},
         "fwd_tflops": round(f_fwd / (stage_avg["fwd"] * 1e-3) / 1e12, 2),
@@ -534,6 +613,8 @@ def main() -> int:
     if not fwd_only:
         res["bwd_tflops"] = round(f_bwd / ((ms_per_step - stage_avg["fwd"]) * 1e-3) / 1e12, 2)
     res["dscore_handoff"] = handoff
+    if elem == 2 and not fwd_only:
+        res["split_active"] = split
     if handoff:
         # the dQ kernel is then HBM-bound: it streams every stored dS block once
         # (plus K once and the dQ rows)

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MIMIR_PREFIXLM_ABI_VERSION 4
+#define MIMIR_PREFIXLM_ABI_VERSION 5
 
 /* Element types of q/k/v/out/dout/dq/dk/dv (lse and the workspace are float32). */
 enum MimirDType {
@@ -96,7 +96,37 @@ typedef struct MimirPrefixLMFwdParams {
   int64_t gate_stride_token, gate_stride_head;
   void* gated_out;            /* [T, Hq, D]; required with a gate */
   int64_t gated_out_stride_token, gated_out_stride_head;
+  /* Optional low half of the output (NULL: not written; bf16 only): out_lo =
+   * round(O - round(O)) with O the float32 attention output, so out + out_lo
+   * carries ~16 significant bits.  The backward's delta = rowsum(dout * O) reads
+   * it (MimirPrefixLMBwdParams.out_lo); with bf16 O alone that row sum carries
+   * the output's rounding into every dS of the row.  No reference counterpart. */
+  void* out_lo;               /* [T, Hq, D] */
+  int64_t out_lo_stride_token, out_lo_stride_head;
+  int32_t split_mode;         /* enum MimirSplitMode (bf16; P in O = P V) */
+  /* Optional (NULL: none): the forward writes its split decision (0 / 1) here,
+   * and then writes out_lo only when it splits.  Passed to the backward
+   * (MimirPrefixLMBwdParams.split_flag), the backward follows the same decision
+   * without scanning K again and reads out_lo only when it is set. */
+  int32_t* split_flag;        /* device int32 [1] */
 } MimirPrefixLMFwdParams;
+
+/* Whether the bf16 kernels carry the softmax probabilities P and the score
+ * gradients dS as two bf16 halves.  A bf16 MFMA operand keeps 8 significant
+ * bits; split, the operand is hi + lo with lo = round(x - hi) and every product
+ * with it takes one more MFMA (forward O = P V, backward dK = dS^T Q and
+ * dQ = dS K), which removes that rounding from the result.  dQ and dK are sums
+ * of cancelling terms (every row of dS sums to zero) and delta = rowsum(dout * O)
+ * inherits the rounding of O, so with large key or query entries these roundings
+ * dominate the gradients' error.  AUTO splits when softmax_scale * max|K| > 0.75
+ * anywhere in the call: the prologue of the forward and of the backward's DELTA
+ * stage scans K on the device, and the kernels read the result (no host
+ * synchronisation).  No reference counterpart. */
+enum MimirSplitMode {
+  MIMIR_SPLIT_AUTO = 0,
+  MIMIR_SPLIT_ALWAYS = 1,
+  MIMIR_SPLIT_NEVER = 2
+};
 
 typedef struct MimirPrefixLMBwdParams {
   const void* q;
@@ -148,12 +178,26 @@ typedef struct MimirPrefixLMBwdParams {
    * this many bytes of workspace (mimir_prefixlm_bwd_dscore_bytes), the DKDV
    * stage writes them there and the DQ stage computes dQ = dS K from them
    * instead of recomputing S and dP; DQ then reads what DKDV wrote and runs
-   * after it.  0: DQ recomputes. */
+   * after it.  0: DQ recomputes.  The stored tiles carry no low half, so when
+   * dS is split (split_mode) the recomputing dQ kernel runs instead: for ALWAYS
+   * the hand-off is off, for AUTO both dQ kernels are enqueued and the one the
+   * device-side decision selects does the work (the other exits at once).  The
+   * recompute also takes over when a stored tile would fall outside the region
+   * (a sequence longer than max_seqlen_all). */
   size_t dscore_limit_bytes;
+  /* Low half of the forward output (NULL: delta from out alone; with split_flag
+   * read only when the flag is set); see MimirPrefixLMFwdParams.out_lo. */
+  const void* out_lo;         /* [T, Hq, D] */
+  int64_t out_lo_stride_token, out_lo_stride_head;
+  int32_t split_mode;         /* enum MimirSplitMode (bf16; dS in dK = dS^T Q and dQ = dS K) */
+  const int32_t* split_flag;  /* the forward's recorded decision (device int32 [1]) or NULL */
 } MimirPrefixLMBwdParams;
 
 /* Bytes of device workspace the forward needs: the heaviest-first tile work list
- * (int32 pairs, one per 128-row query tile of every sequence). */
+ * (int32 pairs, one per 128-row query tile of every sequence; sized
+ * ceil(T / 128) + numseqs, which bounds the tiles of any packing of T tokens into
+ * numseqs sequences, so it does not rely on max_seqlen_all), then, 256-byte
+ * aligned, the 512 int32 slots of the K scan behind split_mode AUTO. */
 size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs, int32_t max_seqlen_all);
 
 /* Forward: out (and lse if non-NULL).
@@ -287,13 +331,17 @@ typedef struct MimirCacheAttnParams {
 size_t mimir_prefixlm_cache_attn_workspace_bytes(const MimirCacheAttnParams* params);
 int mimir_prefixlm_cache_attn(const MimirCacheAttnParams* params, void* stream);
 
-/* Device-side metadata check: writes to *bad_seq (device int32) the first s in
- * [0, numseqs) with prefix_lens[s] + causal_lens[s] != cu_seqlens[s+1] - cu_seqlens[s]
- * or a negative length, or -1 if none.  The reference raises ValueError for this
- * (src/mimir/model/flash_attention_prefixlm_dense.py:54-55).  Asynchronous. */
+/* Device-side metadata check: writes to bad[0] (device int32 [2]) the first s in
+ * [0, numseqs) whose lengths are invalid, or -1 if none, and to bad[1] why:
+ *   1  prefix_lens[s] + causal_lens[s] != cu_seqlens[s+1] - cu_seqlens[s], or a
+ *      negative length (the reference raises ValueError for this,
+ *      src/mimir/model/flash_attention_prefixlm_dense.py:54-55);
+ *   2  cu_seqlens[s+1] - cu_seqlens[s] > max_seqlen_all (the scalar sizes the
+ *      score-gradient region and the per-sequence span check).
+ * Asynchronous. */
 int mimir_prefixlm_check_metadata(const int32_t* prefix_lens, const int32_t* causal_lens,
-                                  const int32_t* cu_seqlens, int32_t numseqs,
-                                  int32_t* bad_seq, void* stream);
+                                  const int32_t* cu_seqlens, int32_t numseqs, int32_t max_seqlen_all,
+                                  int32_t* bad, void* stream);
 
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char* mimir_prefixlm_last_error(void);

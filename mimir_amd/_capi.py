@@ -16,10 +16,14 @@ from pathlib import Path
 
 # MIMIR_PREFIXLM_LIB overrides the in-tree library (e.g. to A/B two builds).
 LIB_PATH = Path(os.environ.get("MIMIR_PREFIXLM_LIB") or Path(__file__).resolve().parent / "_lib" / "libmimir_prefixlm.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_FLOAT32 = 0
 DTYPE_BFLOAT16 = 1
+
+SPLIT_AUTO = 0
+SPLIT_ALWAYS = 1
+SPLIT_NEVER = 2
 
 OK = 0
 ERR_INVALID_ARGUMENT = 1
@@ -47,6 +51,8 @@ class FwdParams(ctypes.Structure):
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("gate", _vp), ("gate_stride_token", _i64), ("gate_stride_head", _i64),
         ("gated_out", _vp), ("gated_out_stride_token", _i64), ("gated_out_stride_head", _i64),
+        ("out_lo", _vp), ("out_lo_stride_token", _i64), ("out_lo_stride_head", _i64),
+        ("split_mode", _i32), ("split_flag", _vp),
     ]
 
 
@@ -71,6 +77,8 @@ class BwdParams(ctypes.Structure):
         ("gate", _vp), ("gate_stride_token", _i64), ("gate_stride_head", _i64),
         ("dgate", _vp), ("dgate_stride_token", _i64), ("dgate_stride_head", _i64),
         ("dscore_limit_bytes", ctypes.c_size_t),
+        ("out_lo", _vp), ("out_lo_stride_token", _i64), ("out_lo_stride_head", _i64),
+        ("split_mode", _i32), ("split_flag", _vp),
     ]
 
 
@@ -165,7 +173,7 @@ def load() -> ctypes.CDLL:
         lib.mimir_prefixlm_cache_attn.restype = ctypes.c_int
         lib.mimir_prefixlm_cache_attn_workspace_bytes.argtypes = [ctypes.POINTER(CacheAttnParams)]
         lib.mimir_prefixlm_cache_attn_workspace_bytes.restype = ctypes.c_size_t
-        lib.mimir_prefixlm_check_metadata.argtypes = [_vp, _vp, _vp, _i32, _vp, _vp]
+        lib.mimir_prefixlm_check_metadata.argtypes = [_vp, _vp, _vp, _i32, _i32, _vp, _vp]
         lib.mimir_prefixlm_check_metadata.restype = ctypes.c_int
         lib.mimir_prefixlm_last_error.argtypes = []
         lib.mimir_prefixlm_last_error.restype = ctypes.c_char_p

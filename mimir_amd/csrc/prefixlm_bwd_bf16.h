@@ -42,7 +42,25 @@ struct BwdArgs {
   int ds_rows, ds_width;
   float scale;
   float scale_log2;
+  const int* kscan;  // workspace: the DELTA stage's K magnitude slots (kKScanSlots)
+  const int* split_flag;  // the forward's recorded split decision, or NULL
+  int split_mode;    // MimirSplitMode
+  int dq_companion;  // 1: the recomputing dQ kernel enqueued beside the hand-off's
 };
+
+// queue[kDsIncomplete]: set by the dK / dV kernel when a score-gradient tile fell
+// outside the region (zeroed by the DELTA stage with the other counters).
+constexpr int kDsIncomplete = 2;
+
+// Whether the dK and dQ products split dS into bf16 hi + lo (wave-uniform).
+__device__ __forceinline__ bool split_on(const BwdArgs& a, int lane) {
+  return split_decision(a.split_mode, a.kscan, a.split_flag, lane);
+}
+// With the score-gradient hand-off, whether the recomputing dQ kernel does the
+// work instead of the one that reads the stored tiles (which have no low half).
+__device__ __forceinline__ bool dq_needs_recompute(const BwdArgs& a, bool split) {
+  return split || a.queue[kDsIncomplete] != 0;
+}
 
 
 // Each launcher computes its own grid from the geometry in `a` and enqueues one

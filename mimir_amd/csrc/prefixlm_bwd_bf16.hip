@@ -86,10 +86,17 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   a.is_causal = p.is_causal;
   a.scale = p.softmax_scale;
   a.scale_log2 = p.softmax_scale * kLog2e;
+  a.kscan = (const int*)(wsb + ws.kscan);
+  a.split_flag = p.split_flag;
+  a.split_mode = p.split_mode;
+  a.dq_companion = 0;
 
   if (stages & MIMIR_BWD_STAGE_DELTA) {
     DeltaArgs& d = pro.delta;
     d.o = a.o; d.dout = (const bf16_t*)p.dout; d.lse = a.lse; d.delta = a.delta; d.lse2 = a.lse2;
+    d.o_lo = (const bf16_t*)p.out_lo;
+    d.lo_gate = p.split_flag;
+    d.olo_st = p.out_lo_stride_token; d.olo_sh = p.out_lo_stride_head;
     d.o_st = a.o_st; d.o_sh = a.o_sh; d.do_st = p.dout_stride_token; d.do_sh = p.dout_stride_head;
     d.lse_sh = a.lse_sh;
     d.T = a.T; d.Hq = a.Hq; d.D = D;
@@ -108,11 +115,15 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
       pk.max_pairs = ws.pair_heads / a.Hkv;
       pk.slots = device_cu_count();
     }
-    pk.zero = a.split_ctr;  // split counters and the dK / dV work queue
-    pk.n_zero = ws.pair_heads + 2;
+    pk.zero = a.split_ctr;  // split counters, the dK / dV work queue and the dS-incomplete flag
+    pk.n_zero = ws.pair_heads + kCounterWordsAfterPairs;
     pro.plan[pro.nplan++] = pk;
     pro.plan[pro.nplan++] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
                                       p.total_tokens, /*kind=*/0, a.group, a.cap_q, a.plan_q);
+    if (p.split_mode == MIMIR_SPLIT_AUTO && p.split_flag == nullptr) {  // no recorded decision: scan K
+      pro.kscan = kscan_args(a.k, a.k_st, a.k_sh, a.T, a.Hkv, D, p.softmax_scale, (int*)(wsb + ws.kscan));
+      pro.has_kscan = 1;
+    }
   }
   hipError_t e = launch_prologue(pro, stream);
   if (e != hipSuccess) return e;

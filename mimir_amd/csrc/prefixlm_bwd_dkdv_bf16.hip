@@ -26,7 +26,9 @@ struct DkCfg {
   static constexpr int kWavesPerSimd = 2;
 };
 
-template <int D>
+// kSplit: dS as bf16 hi + lo in the dK product.  With split_mode AUTO both
+// instantiations are enqueued and the one the K scan does not select exits at once.
+template <int D, bool kSplit>
 __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) void dkdv_kernel(const BwdArgs a) {
   constexpr int DT = D / 32;
   constexpr int KS = D / 16;
@@ -55,6 +57,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   const int rank = blockIdx.x / a.Hkv;
   const int hk = blockIdx.x - rank * a.Hkv;
   const int4 item = a.plan_k[rank];  // never split for this kernel: part 0
+  if (split_on(a, lane) != kSplit) return;
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int ktile = item.y;
@@ -187,17 +190,19 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
       __builtin_amdgcn_sched_barrier(0);
       // rows of sc / dp: query 32*mt + 8*(r/4) + 4*hi + r%4 ; column: the lane's key.
       if (masked) {
-        // allowed iff qs_lane <= q < nq, i.e. (unsigned)(q - qs_lane) < (unsigned)(nq - qs_lane).
-        // The empty volatile asm keeps this block a real branch: if-converted, its
-        // 48 VALU operations would run on every unmasked tile as well.
+        // allowed iff qs_lane <= q < nq, i.e. (unsigned)(q - qs_lane) < (unsigned)max(nq - qs_lane, 0):
+        // a key past the last active query (nq < qs_lane, total_seqlen ending inside
+        // the sequence) has no allowed query at all.  The empty volatile asm keeps
+        // this block a real branch: if-converted, its 48 VALU operations would run on
+        // every unmasked tile as well.
         __asm__ volatile("");
         const unsigned base = (unsigned)(qb + 32 * mt + 4 * hi - qs_lane);
-        const unsigned lim = (unsigned)(g.nq - qs_lane);
+        const unsigned lim = (unsigned)max(g.nq - qs_lane, 0);
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if (base + (unsigned)(8 * (r >> 2) + (r & 3)) >= lim) sc[r] = -INFINITY;
       }
-      bf16x8 pb[2], db[2];
+      bf16x8 pb[2], db[2], dl[kSplit ? 2 : 1];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         f32x8 tp, tds;
@@ -217,6 +222,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
         }
         pb[s2] = to_bf16x8(tp);
         db[s2] = to_bf16x8(tds);
+        if constexpr (kSplit) dl[s2] = lo_half(tds, db[s2]);
       }
       __builtin_amdgcn_sched_barrier(0);
       if (mt == 0) load_s(1);
@@ -226,6 +232,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
         for (int dt = 0; dt < DT; ++dt) {
           dvacc[dt] = mfma32(ot[s2][dt], pb[s2], dvacc[dt]);
           dkacc[dt] = mfma32(qt[s2][dt], db[s2], dkacc[dt]);
+          if constexpr (kSplit) dkacc[dt] = mfma32(qt[s2][dt], dl[s2], dkacc[dt]);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -275,14 +282,20 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
 }
 
 
+template __global__ void dkdv_kernel<64, false>(const BwdArgs);
+template __global__ void dkdv_kernel<64, true>(const BwdArgs);
+
 template <int D>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   constexpr int kDkKeys = DkCfg<D>::kKeys, kDkWaves = DkCfg<D>::kWaves;
   static_assert(kDkKeys == kPlanTile, "work-list tiles are the dK / dV key tiles");
   if (numseqs <= 0 || a.cap_k == 0) return hipSuccess;
-  // workgroup r * Hkv + h: list entry r, kv head h
-  hipLaunchKernelGGL((dkdv_kernel<D>), dim3((unsigned)a.cap_k * (unsigned)a.Hkv), dim3(kDkWaves * 64), 0,
-                     stream, a);
+  // workgroup r * Hkv + h: list entry r, kv head h; AUTO enqueues both instantiations
+  const dim3 grid((unsigned)a.cap_k * (unsigned)a.Hkv);
+  void (*const plain)(BwdArgs) = dkdv_kernel<D, false>;
+  void (*const split)(BwdArgs) = dkdv_kernel<D, true>;
+  if (a.split_mode != MIMIR_SPLIT_ALWAYS) hipLaunchKernelGGL(plain, grid, dim3(kDkWaves * 64), 0, stream, a);
+  if (a.split_mode != MIMIR_SPLIT_NEVER) hipLaunchKernelGGL(split, grid, dim3(kDkWaves * 64), 0, stream, a);
   return hipGetLastError();
 }
 

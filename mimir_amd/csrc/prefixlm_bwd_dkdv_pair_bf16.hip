@@ -28,7 +28,7 @@ constexpr int kNonTemporal = 2;  // buffer cache policy: streaming (nt)
 constexpr int kPairKeys = 128;
 constexpr int kPairD = 128;
 
-template <bool kStoreDs>
+template <bool kStoreDs, bool kSplit>
 __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   constexpr int D = kPairD;
   constexpr int DT = D / 32;
@@ -70,6 +70,9 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   const Loader ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane), ldv(a.v_st, wave, lane);
   const TileLanes<D> tl(lane);
   const float c2 = a.scale_log2;
+  // kSplit: dS as bf16 hi + lo in the dK product.  With split_mode AUTO both
+  // instantiations are enqueued and the one the K scan does not select exits here.
+  if (split_on(a, lane) != kSplit) return;
   auto fetch_unit = [&]() {  // next work unit from the launch-wide queue
     return (int)gridDim.x + __hip_atomic_fetch_add(&a.queue[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
@@ -99,9 +102,16 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   const int n_iter = (half == 1 ? n_all / 2 : n_all) - it_lo;
   const int head0 = nqt > 0 ? it_lo / nqt : 0;  // first step: q head hk * G + head0, query tile tile0
   const int tile0 = it_lo - head0 * nqt;
-  // dS blocks of this wave: key block ka / 32 of block row floor(start / 32) + s + query / 32
+  // dS blocks of this wave: key block ka / 32 of block row floor(start / 32) + s + query / 32.
+  // A unit whose blocks do not all fit the region (a sequence longer than
+  // max_seqlen_all) stores none and flags the hand-off incomplete: the
+  // recomputing dQ kernel then takes over.
   const int ds_row0 = g.start / kDsBlock + s;
-  const bool ds_key_ok = (ka >> 5) < a.ds_width;
+  bool ds_unit_ok = true;
+  if constexpr (kStoreDs) {
+    ds_unit_ok = (ka >> 5) < a.ds_width && (g.nq <= 0 || ds_row0 + (g.nq - 1) / kDsBlock < a.ds_rows);
+    if (!ds_unit_ok && wave_active && lane == 0) a.queue[kDsIncomplete] = 1;
+  }
 
   const bf16_t* kseq = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
   const bf16_t* vseq = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
@@ -235,16 +245,17 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     __builtin_amdgcn_s_setprio(0);
     // rows of sc / dp: query qr + 8*(r/4) + 4*hi + r%4 ; column: the lane's key.
     if (masked) {
-      // allowed iff qs_lane <= q < nq.  The empty volatile asm keeps this a real
-      // branch, so unmasked tiles do not pay for the compares.
+      // allowed iff qs_lane <= q < nq, i.e. (unsigned)(q - qs_lane) < (unsigned)max(nq - qs_lane, 0)
+      // (no query at all for a key past the last active one).  The empty volatile
+      // asm keeps this a real branch, so unmasked tiles do not pay for the compares.
       __asm__ volatile("");
       const unsigned base = (unsigned)(qr + 4 * hi - qs_lane);
-      const unsigned lim = (unsigned)(g.nq - qs_lane);
+      const unsigned lim = (unsigned)max(g.nq - qs_lane, 0);
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (base + (unsigned)(8 * (r >> 2) + (r & 3)) >= lim) sc[r] = -INFINITY;
     }
-    bf16x8 pb[2], db[2];
+    bf16x8 pb[2], db[2], dl[kSplit ? 2 : 1];
     // dS half s2 (positions 16 s2 .. + 15 of the block: 1 KiB of 32 key rows
     // of 32 bytes) to key row l32, positions 16 s2 + 8 hi + 0..7: one store
     // instruction writes 1 KiB contiguously, non-temporal (cache policy nt):
@@ -255,7 +266,7 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     if constexpr (kStoreDs) {
       const int row = ds_row0 + (qr >> 5);
       const int64_t blk = ((int64_t)(hk * a.group + head) * a.ds_rows + row) * a.ds_width + (ka >> 5);
-      rds = make_rsrc(a.dscore + blk * kDsBlockElems, ds_key_ok && row < a.ds_rows ? kDsBlockElems * 2 : 0);
+      rds = make_rsrc(a.dscore + blk * kDsBlockElems, ds_unit_ok ? kDsBlockElems * 2 : 0);
     }
     auto store_ds = [&](int s2) {
       if constexpr (kStoreDs)
@@ -266,6 +277,7 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     softmax(0, 1);
     pb[0] = to_bf16x8(tp);
     db[0] = to_bf16x8(tds);
+    if constexpr (kSplit) dl[0] = lo_half(tds, db[0]);
     store_ds(0);
     rd_ld(1);
     // Eight dV / dK MFMA pairs; the softmax of the second 16-query step runs
@@ -277,11 +289,13 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
       const int dt = j & 3, s2 = j >> 2;
       dvacc[dt] = mfma32(ot[j % 3], pb[s2], dvacc[dt]);
       dkacc[dt] = mfma32(qt[j % 3], db[s2], dkacc[dt]);
+      if constexpr (kSplit) dkacc[dt] = mfma32(qt[j % 3], dl[s2], dkacc[dt]);
       if (j == 1) softmax(1, 0);
       if (j == 2) softmax(1, 1);
       if (j == 3) {
         pb[1] = to_bf16x8(tp);
         db[1] = to_bf16x8(tds);
+        if constexpr (kSplit) dl[1] = lo_half(tds, db[1]);
         store_ds(1);
       }
     }
@@ -475,11 +489,13 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   }
 }
 
+template <bool kSplit>
 __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const BwdArgs a) {
-  dkdv_pair_body<false>(a);
+  dkdv_pair_body<false, kSplit>(a);
 }
+// The hand-off stores unsplit dS: with a split dQ the stored tiles are not used.
 __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_ds_kernel(const BwdArgs a) {
-  dkdv_pair_body<true>(a);
+  dkdv_pair_body<true, false>(a);
 }
 
 }  // namespace
@@ -492,8 +508,14 @@ hipError_t launch_bwd_dkdv_pair_bf16(BwdArgs a, int numseqs, int max_seqlen_all,
   // one persistent workgroup per CU
   const int64_t units = (int64_t)a.cap_k * a.Hkv;
   const int grid = (int)(units < device_cu_count() ? units : device_cu_count());
-  hipLaunchKernelGGL(a.dscore != nullptr ? dkdv_pair_ds_kernel : dkdv_pair_kernel, dim3((unsigned)grid),
-                     dim3(kPairWaves * 64), 0, stream, a);
+  // AUTO: the unsplit and the split instantiation, each exiting at once unless the
+  // K scan selects it (the persistent grid is one workgroup per CU, so the
+  // exiting one costs a few microseconds)
+  if (a.split_mode != MIMIR_SPLIT_ALWAYS)
+    hipLaunchKernelGGL(a.dscore != nullptr ? dkdv_pair_ds_kernel : dkdv_pair_kernel<false>, dim3((unsigned)grid),
+                       dim3(kPairWaves * 64), 0, stream, a);
+  if (a.split_mode != MIMIR_SPLIT_NEVER)
+    hipLaunchKernelGGL(dkdv_pair_kernel<true>, dim3((unsigned)grid), dim3(kPairWaves * 64), 0, stream, a);
   return hipGetLastError();
 }
 

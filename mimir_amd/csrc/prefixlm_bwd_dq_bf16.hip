@@ -43,6 +43,10 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   const int m0 = qtile * kBlockQ;
   if (m0 >= g.nq) return;
   const int hk = h / a.group;
+  // dS split into bf16 hi + lo for the dQ product (wave-uniform); beside the
+  // score-gradient hand-off this kernel works only when the hand-off cannot.
+  const bool split = split_on(a, lane);
+  if (a.dq_companion && !dq_needs_recompute(a, split)) return;
 
   const int wg_kend = max(g.p, min(m0 + kBlockQ, g.nq));
   const int nkt = (wg_kend + kBlockK - 1) / kBlockK;
@@ -51,7 +55,6 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   const int w_kend_max = wave_active ? max(g.p, min(qa + 32, g.nq)) : 0;
   const int w_kend_min = max(g.p, qa + 1);
   const int qpos = qa + l32;
-  const int kend_lane = kend_of(g.p, qpos);
 
   const __amdgpu_buffer_rsrc_t rq =
       make_rsrc(a.q + (int64_t)g.start * a.q_st + (int64_t)h * a.q_sh, rows_bytes(g.nq, a.q_st, D));
@@ -114,13 +117,15 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
       // The empty volatile asm keeps this a real branch, so unmasked tiles do not
       // pay for the compares.
       __asm__ volatile("");
+      // kpos >= kend(qpos) with kpos = kb + 32 mt + 8 (r / 4) + 4 hi + r % 4; the
+      // lane terms are rebuilt here rather than kept in a register across the loop
+      const int ln = opaque_lane_id();
+      const int base = kb + 4 * (ln >> 5) - kend_of(g.p, qa + (ln & 31));
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kpos = kb + 32 * mt + 8 * (r >> 2) + 4 * hi + (r & 3);
-          if (kpos >= kend_lane) st[mt][r] = -INFINITY;
-        }
+        for (int r = 0; r < 16; ++r)
+          if (base + 32 * mt + 8 * (r >> 2) + (r & 3) >= 0) st[mt][r] = -INFINITY;
     }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -129,7 +134,9 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
         const float pr = fast_exp2(__builtin_fmaf(st[mt][r], c2, -lse2));
         st[mt][r] = pr * (dpt[mt][r] - dlt);
       }
-    bf16x8 sf[4];
+    // dQ^T += K^T dS^T; split: dS = hi + lo with lo = round(dS - hi), one more
+    // MFMA per K^T fragment (the rounding of dS then no longer reaches dQ).
+    bf16x8 sf[4], sl[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int mt = kk >> 1, s8 = (kk & 1) * 8;
@@ -137,17 +144,31 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) t[e] = st[mt][s8 + e];
       sf[kk] = to_bf16x8(t);
-    }
+      if (split) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16_t* kp = &sK[tl.tr_base + kk * 16 * L::kRowElems + dt * 32];
-        const bf16x4 k0 = lds_read_tr16(kp);
-        const bf16x4 k1 = lds_read_tr16(kp + L::kTrSecond);
-        dqacc[dt] = mfma32(cat8(k0, k1), sf[kk], dqacc[dt]);
+        for (int e = 0; e < 8; ++e) t[e] -= (float)sf[kk][e];
+        sl[kk] = to_bf16x8(t);
       }
     }
+    auto dq_mfmas = [&](auto split_tag) {
+      constexpr bool kSplit = decltype(split_tag)::value;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const bf16_t* kp = &sK[tl.tr_base + kk * 16 * L::kRowElems + dt * 32];
+          const bf16x4 k0 = lds_read_tr16(kp);
+          const bf16x4 k1 = lds_read_tr16(kp + L::kTrSecond);
+          const bf16x8 kt = cat8(k0, k1);
+          dqacc[dt] = mfma32(kt, sf[kk], dqacc[dt]);
+          if constexpr (kSplit) dqacc[dt] = mfma32(kt, sl[kk], dqacc[dt]);
+        }
+      }
+    };
+    if (split)
+      dq_mfmas(BoolTag<true>{});
+    else
+      dq_mfmas(BoolTag<false>{});
   };
 
   for (int kt = 0; kt < nkt; kt += 2) {
@@ -206,7 +227,16 @@ hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream
 }  // namespace
 
 hipError_t launch_bwd_dq_bf16(const BwdArgs& a, int head_dim, int numseqs, int max_seqlen_all, hipStream_t stream) {
-  if (head_dim == 128 && a.dscore != nullptr) return launch_bwd_dq_ds_bf16(a, numseqs, stream);
+  if (head_dim == 128 && a.dscore != nullptr) {
+    // dQ from the stored tiles, and beside it the recomputing kernel, which
+    // works only when the device-side checks rule the stored tiles out (dS split,
+    // or a tile that did not fit the region); otherwise its workgroups exit at once.
+    hipError_t e = launch_bwd_dq_ds_bf16(a, numseqs, stream);
+    if (e != hipSuccess) return e;
+    BwdArgs c = a;
+    c.dq_companion = 1;
+    return launch<128>(c, numseqs, max_seqlen_all, stream);
+  }
   switch (head_dim) {
     case 64: return launch<64>(a, numseqs, max_seqlen_all, stream);
     case 128: return launch<128>(a, numseqs, max_seqlen_all, stream);

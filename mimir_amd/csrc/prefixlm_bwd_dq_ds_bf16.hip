@@ -57,6 +57,9 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
   const int m0 = qtile * kBlockQ;
   if (m0 >= g.nq) return;
   const int hk = h / a.group;
+  // The stored tiles carry no low half and may be incomplete: the recomputing
+  // dQ kernel enqueued beside this one does the work then.
+  if (dq_needs_recompute(a, split_on(a, lane))) return;
 
   const int wg_kend = max(g.p, min(m0 + kBlockQ, g.nq));
   const int nkt = (wg_kend + kBlockK - 1) / kBlockK;

@@ -16,15 +16,25 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
+}  // namespace
+
+namespace mimir {
+int fail_with(int code, const std::string& msg) { return fail(code, msg); }
+}  // namespace mimir
+
+namespace {
+
 int hip_status(hipError_t e, const char* what) {
   if (e == hipSuccess) return MIMIR_OK;
   return fail(MIMIR_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// bad[0]: the first invalid sequence (-1: none); bad[1]: 1 for inconsistent or
+// negative lengths, 2 for a length above max_seqlen_all.
 __global__ __launch_bounds__(256) void check_metadata_kernel(const int32_t* prefix_lens,
                                                               const int32_t* causal_lens,
                                                               const int32_t* cu_seqlens, int numseqs,
-                                                              int32_t* bad_seq) {
+                                                              int max_seqlen_all, int32_t* bad) {
   __shared__ int best;
   if (threadIdx.x == 0) best = 0x7fffffff;
   __syncthreads();
@@ -32,11 +42,21 @@ __global__ __launch_bounds__(256) void check_metadata_kernel(const int32_t* pref
   for (int s = threadIdx.x; s < numseqs; s += blockDim.x) {
     const int len = cu_seqlens[s + 1] - cu_seqlens[s];
     const int p = prefix_lens[s], c = causal_lens[s];
-    if (len < 0 || p < 0 || c < 0 || p + c != len) { mine = s; break; }
+    if (len < 0 || p < 0 || c < 0 || p + c != len || len > max_seqlen_all) { mine = s; break; }
   }
   atomicMin(&best, mine);
   __syncthreads();
-  if (threadIdx.x == 0) *bad_seq = best == 0x7fffffff ? -1 : best;
+  if (threadIdx.x == 0) {
+    const int s = best == 0x7fffffff ? -1 : best;
+    int why = 0;
+    if (s >= 0) {
+      const int len = cu_seqlens[s + 1] - cu_seqlens[s];
+      const int p = prefix_lens[s], c = causal_lens[s];
+      why = (len < 0 || p < 0 || c < 0 || p + c != len) ? 1 : 2;
+    }
+    bad[0] = s;
+    bad[1] = why;
+  }
 }
 
 int elem_bytes_of(int dtype) { return dtype == MIMIR_DTYPE_FLOAT32 ? 4 : 2; }
@@ -97,13 +117,15 @@ const char* mimir_prefixlm_last_error(void) { return g_last_error.c_str(); }
 int mimir_prefixlm_abi_version(void) { return MIMIR_PREFIXLM_ABI_VERSION; }
 
 size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs, int32_t max_seqlen_all) {
-  if (total_tokens <= 0) return 0;
-  return (size_t)mimir::plan_capacity(total_tokens, numseqs, max_seqlen_all) * sizeof(int2);
+  const int cap = mimir::plan_capacity(total_tokens, numseqs, max_seqlen_all);
+  if (cap <= 0) return 0;
+  return mimir::fwd_kscan_offset(cap) + (size_t)mimir::kKScanSlots * sizeof(int);
 }
 
 size_t mimir_prefixlm_bwd_dscore_bytes(const MimirPrefixLMBwdParams* p) {
+  // the stored tiles have no low half: no hand-off when dS is always split
   if (p == nullptr || p->dtype != MIMIR_DTYPE_BFLOAT16 || p->head_dim != 128 || p->total_tokens <= 0 ||
-      p->num_q_heads <= 0 || p->dscore_limit_bytes == 0)
+      p->num_q_heads <= 0 || p->dscore_limit_bytes == 0 || p->split_mode == MIMIR_SPLIT_ALWAYS)
     return 0;
   const mimir::DscoreGeom g = mimir::dscore_geometry(p->total_tokens, p->num_q_heads, p->numseqs, p->max_seqlen_all);
   return g.bytes <= p->dscore_limit_bytes ? g.bytes : 0;
@@ -129,15 +151,15 @@ size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_he
 }
 
 int mimir_prefixlm_check_metadata(const int32_t* prefix_lens, const int32_t* causal_lens,
-                                  const int32_t* cu_seqlens, int32_t numseqs, int32_t* bad_seq,
-                                  void* stream) {
+                                  const int32_t* cu_seqlens, int32_t numseqs, int32_t max_seqlen_all,
+                                  int32_t* bad, void* stream) {
   g_last_error.clear();
-  if (bad_seq == nullptr) return fail(MIMIR_ERR_INVALID_ARGUMENT, "bad_seq is NULL");
+  if (bad == nullptr) return fail(MIMIR_ERR_INVALID_ARGUMENT, "bad is NULL");
   if (numseqs < 0) return fail(MIMIR_ERR_INVALID_ARGUMENT, "negative numseqs");
   if (numseqs > 0 && (prefix_lens == nullptr || causal_lens == nullptr || cu_seqlens == nullptr))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "metadata pointer is NULL");
   hipLaunchKernelGGL(check_metadata_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, prefix_lens,
-                     causal_lens, cu_seqlens, numseqs, bad_seq);
+                     causal_lens, cu_seqlens, numseqs, max_seqlen_all, bad);
   return hip_status(hipGetLastError(), "metadata check launch");
 }
 
@@ -168,10 +190,23 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* p, void* stream_) {
                             rows)))
       return rc;
   }
+  if (p->split_mode < MIMIR_SPLIT_AUTO || p->split_mode > MIMIR_SPLIT_NEVER)
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "split_mode must be MIMIR_SPLIT_AUTO, _ALWAYS or _NEVER");
+  if (((uintptr_t)p->split_flag & 3u) != 0) return fail(MIMIR_ERR_INVALID_ARGUMENT, "split_flag must be 4-byte aligned");
+  if (p->out_lo != nullptr) {
+    if (dt != MIMIR_DTYPE_BFLOAT16)
+      return fail(MIMIR_ERR_INVALID_ARGUMENT, "out_lo is a bfloat16 output (float32 needs no low half)");
+    if ((rc = check_operand("out_lo", p->out_lo, p->out_lo_stride_token, p->out_lo_stride_head, D, dt, rows)))
+      return rc;
+  }
   mimir::Prologue pro;
   pro.fill[pro.nfill++] = mimir::fill_args(p->out, p->out_stride_token, p->out_stride_head, p->lse,
                                            p->lse_stride_head, p->cu_seqlens, p->numseqs, p->total_seqlen,
                                            p->total_tokens, p->num_q_heads, D, elem_bytes_of(dt));
+  if (p->out_lo != nullptr)  // padding rows: O = 0 exactly, so its low half is 0
+    pro.fill[pro.nfill++] = mimir::fill_args(p->out_lo, p->out_lo_stride_token, p->out_lo_stride_head, nullptr, 0,
+                                             p->cu_seqlens, p->numseqs, p->total_seqlen, p->total_tokens,
+                                             p->num_q_heads, D, elem_bytes_of(dt));
   hipError_t e;
   if (dt == MIMIR_DTYPE_BFLOAT16) {
     // gated_out rows outside the attended rows are sigmoid(gate) * 0 = 0
@@ -220,6 +255,15 @@ int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* p, int stages, void*
     if ((rc = check_operand("dgate", p->dgate, p->dgate_stride_token, p->dgate_stride_head, D, dt, rows)))
       return rc;
   }
+  if (p->out_lo != nullptr) {
+    if (dt != MIMIR_DTYPE_BFLOAT16)
+      return fail(MIMIR_ERR_INVALID_ARGUMENT, "out_lo is a bfloat16 input (float32 needs no low half)");
+    if ((rc = check_operand("out_lo", p->out_lo, p->out_lo_stride_token, p->out_lo_stride_head, D, dt, rows)))
+      return rc;
+  }
+  if (p->split_mode < MIMIR_SPLIT_AUTO || p->split_mode > MIMIR_SPLIT_NEVER)
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "split_mode must be MIMIR_SPLIT_AUTO, _ALWAYS or _NEVER");
+  if (((uintptr_t)p->split_flag & 3u) != 0) return fail(MIMIR_ERR_INVALID_ARGUMENT, "split_flag must be 4-byte aligned");
   const size_t need = mimir_prefixlm_bwd_workspace_size(p);
   if (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +

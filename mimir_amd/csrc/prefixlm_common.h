@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
 #include "../../include/mimir_prefixlm.h"
 
 namespace mimir {
@@ -100,6 +102,15 @@ __device__ __forceinline__ i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
 }
 __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+// The lane id, formed by instructions the compiler cannot see through: a value
+// derived from it is recomputed where it is used instead of being held in a
+// register (or spilled) across a loop.
+__device__ __forceinline__ int opaque_lane_id() {
+  int l;
+  __asm__ volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -301,7 +312,13 @@ namespace mimir {
 // dK / dV (see SplitSlots).  Splitting evens out the workgroups when a few
 // heavy key tiles (the prefix tiles, which every query attends) dominate.
 constexpr int kPlanTile = 128;
+// List entries for any packing of total_tokens tokens into numseqs sequences:
+// sum_s ceil(n_s / 128) <= ceil(T / 128) + numseqs.  max_seqlen_all is not used,
+// so metadata with an understated max_seqlen_all still lists every tile.
 int plan_capacity(int total_tokens, int numseqs, int max_seqlen_all);
+// Forward workspace: the work list (int2 [cap]), then at this 256-byte aligned
+// offset the kKScanSlots int32 slots of the K scan.
+inline size_t fwd_kscan_offset(int cap) { return ((size_t)(cap > 0 ? cap : 0) * 8 + 255) & ~(size_t)255; }
 
 struct PlanArgs {
   const int32_t* cu_seqlens;
@@ -323,10 +340,23 @@ struct PlanArgs {
 constexpr int kSplitPairHeads = 384;              // most (pair, kv head) combinations per call
 constexpr int kSplitSlotFloats = 2 * 128 * 128;   // dK + dV partial of one part
 
+// Device-side choice of the split products (MimirSplitMode).  The forward's
+// prologue (and the backward's DELTA stage when no forward decision is given)
+// scans K in kKScanSlots workgroups; slot b is 1 if its share holds an element
+// with softmax_scale * |k| > kSplitThreshold.  With AUTO the kernels carry P
+// (forward) and dS (backward) as bf16 hi + lo when any slot is set; the forward
+// records that decision in a one-word flag the backward reads.  The backward's counter words after the
+// split counters and the work queue hold one more flag: non-zero when the dK / dV
+// kernel could not store a score-gradient tile (a sequence longer than
+// max_seqlen_all), so that the recomputing dQ kernel takes over from the hand-off.
+constexpr int kKScanSlots = 512;
+constexpr float kSplitThreshold = 0.75f;
+constexpr int kCounterWordsAfterPairs = 3;  // work queue next / finished, dS-incomplete flag
+
 // Backward workspace sections (byte offsets, 256-byte aligned).
 // `dout_bytes`: the gated backward's upstream-gradient buffer (0 without a gate).
 struct BwdWorkspace {
-  size_t delta, lse2, plan_q, plan_k, counters, slots, dout, dscore, total;
+  size_t delta, lse2, plan_q, plan_k, counters, kscan, slots, dout, dscore, total;
   int cap_q, cap_k, pair_heads;
 };
 BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all,
@@ -367,6 +397,9 @@ __host__ __device__ constexpr int ds_query_of(int pos) { return (pos & ~12) | ((
 // uses) and dgate = round(round(dout * O) * (1 - s) * s), s = round(sigmoid(gate)).
 struct DeltaArgs {
   const bf16_t* o;
+  const bf16_t* o_lo;  // optional low half of O (delta from O + O_lo) ...
+  const int* lo_gate;  // ... read only if this flag (the forward's split decision) is set; NULL: always
+  int64_t olo_st, olo_sh;
   const bf16_t* dout;
   const float* lse;
   float* delta;
@@ -390,11 +423,45 @@ struct FillArgs {
   int numseqs, total_seqlen, T, H, row_bytes, elem_bytes;
 };
 
+// K magnitude scan for the dQ split decision (see kKScanSlots): kKScanSlots
+// workgroups, each over a strided share of the [T, Hkv, D] rows.
+struct KScanArgs {
+  const bf16_t* k;
+  int64_t k_st, k_sh;
+  int T, Hkv, D;
+  uint32_t thr_bits;  // bf16 magnitude bits of kSplitThreshold / softmax_scale
+  int* slots;         // [kKScanSlots]
+};
+
+KScanArgs kscan_args(const bf16_t* k, int64_t k_st, int64_t k_sh, int T, int Hkv, int D, float scale, int* slots);
+
+// Whether a kernel splits its bf16 operand (wave-uniform): always, never, or
+// (AUTO) as the recorded decision `flag` says, or without one when the K scan
+// of this call set any slot.
+__device__ __forceinline__ bool split_decision(int mode, const int* slots, const int* flag, int lane) {
+  static_assert(kKScanSlots == 2 * 64 * 4, "two int4 loads per lane cover the slots");
+  if (mode == MIMIR_SPLIT_ALWAYS) return true;
+  if (mode != MIMIR_SPLIT_AUTO) return false;
+  if (flag != nullptr) return __builtin_amdgcn_readfirstlane(*flag) != 0;
+  const i32x4 a = ((const i32x4*)slots)[lane], b = ((const i32x4*)slots)[lane + 64];
+  const int any = (a[0] | a[1] | a[2] | a[3] | b[0] | b[1] | b[2] | b[3]) != 0;
+  return __builtin_amdgcn_ballot_w64(any) != 0;
+}
+
+// bf16 hi + lo halves of 8 fp32 values: hi = round(x), lo = round(x - hi).
+__device__ __forceinline__ bf16x8 lo_half(f32x8 x, bf16x8 hi) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] -= (float)hi[e];
+  return __builtin_convertvector(x, bf16x8);
+}
+
 struct Prologue {
   PlanArgs plan[2];
   int nplan = 0;
   DeltaArgs delta;
   int has_delta = 0;
+  KScanArgs kscan;
+  int has_kscan = 0;
   FillArgs fill[3];  // targets of one launch share T
   int nfill = 0;
 };
@@ -431,6 +498,11 @@ hipError_t launch_rope(const MimirRopeParams& p, hipStream_t stream);
 hipError_t launch_gate_fwd_f32(const MimirPrefixLMFwdParams& p, hipStream_t stream);
 // float32 gate backward rows: dout_s = dout * s, delta, dgate (one thread per row).
 hipError_t launch_gate_bwd_f32(const MimirPrefixLMBwdParams& p, float* dout_s, float* delta, hipStream_t stream);
+}  // namespace mimir
+
+namespace mimir {
+// Sets the thread-local message mimir_prefixlm_last_error() returns; returns `code`.
+int fail_with(int code, const std::string& msg);
 }  // namespace mimir
 
 // Internal launchers (implemented per kernel file, dispatched from prefixlm_capi.hip).

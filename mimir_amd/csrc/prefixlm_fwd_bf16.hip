@@ -50,9 +50,17 @@ struct FwdArgs {
   const bf16_t* gate;  // optional sigmoid output gate [T, Hq, D]; y = round(round(sigmoid(gate)) * O)
   bf16_t* y;
   int64_t g_st, g_sh, y_st, y_sh;
+  bf16_t* o_lo;        // optional low half: round(O - round(O)), O the fp32 output
+  int64_t olo_st, olo_sh;
+  const int* kscan;    // the prologue's K scan (split_mode AUTO)
+  int split_mode;      // MimirSplitMode: P as bf16 hi + lo in O^T += V^T P^T
+  int* split_flag;     // optional: the decision, for the backward
 };
 
-template <int D, int kGated>
+// kSplit: P is not (0) / is (1) split.  The split changes the registers of the
+// tile loop, so it is a compile-time choice: split_mode AUTO enqueues both
+// instantiations and the one the K scan does not select exits at once.
+template <int D, int kGated, int kSplit>
 __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   constexpr int DT = D / 32;  // 32-row d tiles of O^T
   constexpr int KS = D / 16;  // k-steps of S^T = K Q^T
@@ -71,6 +79,14 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
+
+  // P as bf16 hi + lo in the P V product (wave-uniform): O, and the backward's
+  // delta = rowsum(dO * O), then carry no rounding of P.  Workgroup 0 records
+  // the decision before anything can end it early.
+  const bool split_call = split_decision(a.split_mode, a.kscan, nullptr, lane);
+  if (a.split_flag != nullptr && blockIdx.x == 0 && tid == 0) *a.split_flag = split_call ? 1 : 0;
+  if (split_call != (kSplit == 1)) return;
+  constexpr bool split = kSplit == 1;
 
   const int rank = blockIdx.x / a.Hq;
   const int h = blockIdx.x - rank * a.Hq;
@@ -209,8 +225,9 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
       }
     l_run += lsum;
 
-    // P^T B-operand fragments (16 keys each), key order matching the V^T reads.
-    bf16x8 pf[4];
+    // P^T B-operand fragments (16 keys each), key order matching the V^T reads;
+    // split: the low halves too, one more MFMA per V^T fragment.
+    bf16x8 pf[4], pl[split ? 4 : 1];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int mt = kk >> 1, s8 = (kk & 1) * 8;
@@ -218,8 +235,8 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) t[e] = st[mt][s8 + e];
       pf[kk] = to_bf16x8(t);
+      if constexpr (split) pl[kk] = lo_half(t, pf[kk]);
     }
-
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
@@ -227,7 +244,9 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
         const bf16_t* vp = &sV[tl.tr_base + kk * 16 * L::kRowElems + dt * 32];
         const bf16x4 v0 = lds_read_tr16(vp);
         const bf16x4 v1 = lds_read_tr16(vp + L::kTrSecond);
-        oacc[dt] = mfma32(cat8(v0, v1), pf[kk], oacc[dt]);
+        const bf16x8 vt = cat8(v0, v1);
+        oacc[dt] = mfma32(vt, pf[kk], oacc[dt]);
+        if constexpr (split) oacc[dt] = mfma32(vt, pl[kk], oacc[dt]);
       }
     }
   };
@@ -300,17 +319,43 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
       if constexpr (kGated != 0) *(bf16x8*)&ybase[(int64_t)r * a.y_st] = yv;
     }
   }
+  // The low halves: with a recorded decision only when split (the backward
+  // reads them only then), otherwise always.
+  if (a.o_lo == nullptr || (a.split_flag != nullptr && !split)) return;
+  // Low halves, a second round through the same staging rows (the reads above
+  // are complete before these writes reach LDS: one wave's LDS accesses run in order).
+  __asm__ volatile("" ::: "memory");
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      f32x4 lo;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float t = oacc[dt][4 * rg + e] * inv;
+        lo[e] = t - round_to(t, bf16_t());
+      }
+      *(bf16x4*)&stage[l32 * kPitch + 32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(lo, bf16x4);
+    }
+  __asm__ volatile("" ::: "memory");
+  bf16_t* const lbase = a.o_lo + (int64_t)(g.start + qa) * a.olo_st + (int64_t)h * a.olo_sh + u * 8;
+#pragma unroll
+  for (int j = 0; j < 32 / kRowsPerInst; ++j) {
+    const int r = j * kRowsPerInst + lane / kUnits;
+    const bf16x8 lv = *(const bf16x8*)&stage[r * kPitch + u * 8];
+    if (qa + r < g.nq) *(bf16x8*)&lbase[(int64_t)r * a.olo_st] = lv;
+  }
 }
 
 // Plain and gated stores are separate kernels, so that the gate's pointers stay
 // out of the plain kernel's scalar registers.
-template <int D>
+template <int D, int kSplit>
 __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) {
-  fwd_body<D, 0>(a);
+  fwd_body<D, 0, kSplit>(a);
 }
-template <int D>
+template <int D, int kSplit>
 __global__ __launch_bounds__(kThreads, 2) void fwd_bf16_gated_kernel(const FwdArgs a) {
-  fwd_body<D, 1>(a);
+  fwd_body<D, 1, kSplit>(a);
 }
 
 template <int D>
@@ -339,22 +384,31 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t str
   a.y = (bf16_t*)p.gated_out;
   a.g_st = p.gate_stride_token; a.g_sh = p.gate_stride_head;
   a.y_st = p.gated_out_stride_token; a.y_sh = p.gated_out_stride_head;
+  a.o_lo = (bf16_t*)p.out_lo;
+  a.olo_st = p.out_lo_stride_token; a.olo_sh = p.out_lo_stride_head;
+  a.split_mode = p.split_mode;
+  a.split_flag = p.split_flag;
   static_assert(kBlockM == kPlanTile, "work-list tiles are the forward's query tiles");
   const int cap = plan_capacity(p.total_tokens, p.numseqs, p.max_seqlen_all);
   int2* plan = (int2*)p.workspace;
   a.plan = plan;
-  if (cap > 0)
+  a.kscan = (const int*)((char*)p.workspace + fwd_kscan_offset(cap));
+  if (cap > 0) {
     pro.plan[pro.nplan++] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
                                       p.total_tokens, /*kind=*/0, a.group, cap, plan);
+    if (p.split_mode == MIMIR_SPLIT_AUTO) {  // the K scan behind the split decision
+      pro.kscan = kscan_args(a.k, a.k_st, a.k_sh, a.T, p.num_kv_heads, D, p.softmax_scale, (int*)a.kscan);
+      pro.has_kscan = 1;
+    }
+  }
   hipError_t e = launch_prologue(pro, stream);
   if (e != hipSuccess || cap == 0) return e;
   // workgroup r * Hq + h: list entry r, head h (the heads of one tile back to back)
-  if (a.gate != nullptr)
-    hipLaunchKernelGGL(fwd_bf16_gated_kernel<D>, dim3((unsigned)cap * (unsigned)p.num_q_heads), dim3(kThreads), 0,
-                       stream, a);
-  else
-    hipLaunchKernelGGL(fwd_bf16_kernel<D>, dim3((unsigned)cap * (unsigned)p.num_q_heads), dim3(kThreads), 0,
-                       stream, a);
+  const dim3 grid((unsigned)cap * (unsigned)p.num_q_heads);
+  void (*const plain)(FwdArgs) = a.gate != nullptr ? fwd_bf16_gated_kernel<D, 0> : fwd_bf16_kernel<D, 0>;
+  void (*const split)(FwdArgs) = a.gate != nullptr ? fwd_bf16_gated_kernel<D, 1> : fwd_bf16_kernel<D, 1>;
+  if (p.split_mode != MIMIR_SPLIT_ALWAYS) hipLaunchKernelGGL(plain, grid, dim3(kThreads), 0, stream, a);
+  if (p.split_mode != MIMIR_SPLIT_NEVER) hipLaunchKernelGGL(split, grid, dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

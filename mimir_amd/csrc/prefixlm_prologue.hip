@@ -4,8 +4,11 @@
 // here the workgroups of the three jobs share one grid and run side by side.
 //
 //   workgroups [0, nplan)               one tile work list each
+//   then [0, kscan_blocks)               K magnitude scan (the split decision)
 //   then [0, delta_blocks)               delta = rowsum(O * dO), lse * log2(e)
 //   then nfill x [0, fill_blocks)        zero rows outside every sequence
+// (the single-workgroup lists and the scan go first: they are latency-bound,
+// and dispatched behind thousands of delta workgroups they would end last)
 //
 // Tile work lists: which (sequence, 128-row tile) each workgroup of the forward,
 // dQ and dK/dV kernels takes, heaviest first.  Dispatching (column, tile row)
@@ -46,8 +49,9 @@ constexpr int kFillRows = 16;
 struct PrologueArgs {
   PlanArgs plan[2];
   DeltaArgs delta;
+  KScanArgs kscan;
   FillArgs fill[3];
-  int nplan, delta_blocks, nfill, fill_blocks;
+  int nplan, delta_blocks, kscan_blocks, nfill, fill_blocks;
 };
 
 // Exclusive prefix sum of v over the workgroup; `total` receives the sum.
@@ -236,9 +240,10 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
   constexpr int RPP = kThreads / LPR;   // rows per pass
   const int c = threadIdx.x % LPR;
   const int64_t rows = (int64_t)a.T * a.Hq;
-  bf16x8 ov[kDeltaPasses], dv[kDeltaPasses], gv[kDeltaPasses];
+  bf16x8 ov[kDeltaPasses], dv[kDeltaPasses], gv[kDeltaPasses], lv[kDeltaPasses];
   int t[kDeltaPasses], h[kDeltaPasses];
   bool valid[kDeltaPasses];
+  const bool has_lo = a.o_lo != nullptr && (a.lo_gate == nullptr || *a.lo_gate != 0);
 #pragma unroll
   for (int i = 0; i < kDeltaPasses; ++i) {
     const int64_t row = ((int64_t)b * kDeltaPasses + i) * RPP + threadIdx.x / LPR;  // row = t * Hq + h
@@ -249,6 +254,8 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
       ov[i] = *(const bf16x8*)&a.o[(int64_t)t[i] * a.o_st + (int64_t)h[i] * a.o_sh + c * 8];
       dv[i] = *(const bf16x8*)&a.dout[(int64_t)t[i] * a.do_st + (int64_t)h[i] * a.do_sh + c * 8];
       if constexpr (kGated) gv[i] = *(const bf16x8*)&a.gate[(int64_t)t[i] * a.g_st + (int64_t)h[i] * a.g_sh + c * 8];
+      lv[i] = has_lo ? *(const bf16x8*)&a.o_lo[(int64_t)t[i] * a.olo_st + (int64_t)h[i] * a.olo_sh + c * 8]
+                     : bf16x8{};
     }
   }
 #pragma unroll
@@ -265,13 +272,16 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
           const float dsg = round_to(dy * o, bf16_t());   // gradient of sigmoid(gate)
           ds[e] = (bf16_t)dso;
           dg[e] = (bf16_t)(dsg * (1.0f - s) * s);
-          acc += dso * o;
+          acc += has_lo ? dso * o + dso * (float)lv[i][e] : dso * o;
         }
         *(bf16x8*)&a.dout_s[(int64_t)t[i] * a.ds_st + (int64_t)h[i] * a.ds_sh + c * 8] = ds;
         *(bf16x8*)&a.dgate[(int64_t)t[i] * a.dg_st + (int64_t)h[i] * a.dg_sh + c * 8] = dg;
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += (float)ov[i][e] * (float)dv[i][e];
+        for (int e = 0; e < 8; ++e) {
+          const float dy = (float)dv[i][e];
+          acc += has_lo ? (float)ov[i][e] * dy + (float)lv[i][e] * dy : (float)ov[i][e] * dy;
+        }
       }
     }
 #pragma unroll
@@ -281,6 +291,41 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
       a.lse2[(int64_t)h[i] * a.T + t[i]] = a.lse[(int64_t)h[i] * a.lse_sh + t[i]] * kLog2e;
     }
   }
+}
+
+// K magnitude scan: workgroup b sets slot b to 1 if a bf16 element of its share
+// of the [T, Hkv, D] rows (16-byte units b * 256 + threadIdx.x, then every
+// kKScanSlots * 256 units) has |k| > the threshold, else to 0.  Magnitudes are
+// compared as integers: for finite bf16 the bits with the sign cleared order
+// like the values (a NaN compares above any threshold and sets the slot).
+__device__ void kscan_block(const KScanArgs& a, int b) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const int upr = a.D / 8;  // 16-byte units per row
+  const int64_t units = (int64_t)a.T * a.Hkv * upr;
+  const int64_t step = (int64_t)kKScanSlots * kThreads;
+  u16x2 mx = {0, 0};
+  for (int64_t u0 = (int64_t)b * kThreads + threadIdx.x; u0 < units; u0 += 4 * step) {
+    i32x4 w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // all four loads issued before the first use
+      const int64_t u = u0 + j * step;
+      w[j] = i32x4{0, 0, 0, 0};
+      if (u < units) {
+        const int64_t row = u / upr;
+        const int c = (int)(u - row * upr);
+        const int t = (int)(row / a.Hkv), hk = (int)(row - (int64_t)t * a.Hkv);
+        w[j] = *(const i32x4*)&a.k[(int64_t)t * a.k_st + (int64_t)hk * a.k_sh + c * 8];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2, w[j][e] & 0x7fff7fff));
+  }
+  const int over = (uint32_t)mx[0] > a.thr_bits || (uint32_t)mx[1] > a.thr_bits;
+  const int any = __syncthreads_or(over);
+  if (threadIdx.x == 0) a.slots[b] = any ? 1 : 0;
 }
 
 // Zeroes the padding rows among packed rows [16 b, 16 b + 16) of one tensor.
@@ -313,6 +358,11 @@ __global__ __launch_bounds__(kThreads) void prologue_kernel(const PrologueArgs a
     return;
   }
   b -= a.nplan;
+  if (b < a.kscan_blocks) {
+    kscan_block(a.kscan, b);
+    return;
+  }
+  b -= a.kscan_blocks;
   if constexpr (kDeltaD > 0) {
     if (b < a.delta_blocks) {
       delta_block<kDeltaD, kGated>(a.delta, b);
@@ -326,11 +376,22 @@ __global__ __launch_bounds__(kThreads) void prologue_kernel(const PrologueArgs a
 
 }  // namespace
 
-int plan_capacity(int total_tokens, int numseqs, int max_seqlen_all) {
-  if (numseqs <= 0 || max_seqlen_all <= 0) return 0;
-  const int64_t rect = (int64_t)numseqs * ((max_seqlen_all + kPlanTile - 1) / kPlanTile);
+int plan_capacity(int total_tokens, int numseqs, int /*max_seqlen_all*/) {
+  if (numseqs <= 0 || total_tokens <= 0) return 0;
   const int64_t bound = (int64_t)(total_tokens + kPlanTile - 1) / kPlanTile + numseqs;
-  return (int)(rect < bound ? rect : bound);
+  return (int)(bound < 0x7fffffff ? bound : 0x7fffffff);
+}
+
+KScanArgs kscan_args(const bf16_t* k, int64_t k_st, int64_t k_sh, int T, int Hkv, int D, float scale, int* slots) {
+  KScanArgs ks;
+  ks.k = k; ks.k_st = k_st; ks.k_sh = k_sh;
+  ks.T = T; ks.Hkv = Hkv; ks.D = D;
+  const float thr = kSplitThreshold / scale;  // as bf16 magnitude bits, rounded toward zero
+  uint32_t bits;
+  __builtin_memcpy(&bits, &thr, 4);
+  ks.thr_bits = (bits >> 16) & 0x7fffu;
+  ks.slots = slots;
+  return ks;
 }
 
 PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int numseqs, int total_seqlen,
@@ -368,7 +429,8 @@ BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs
   w.plan_q = align(w.lse2 + rows * sizeof(float));
   w.plan_k = align(w.plan_q + (size_t)w.cap_q * sizeof(int2));
   w.counters = align(w.plan_k + (size_t)w.cap_k * sizeof(int4));
-  w.slots = align(w.counters + ((size_t)w.pair_heads + 2) * sizeof(int));
+  w.kscan = align(w.counters + ((size_t)w.pair_heads + kCounterWordsAfterPairs) * sizeof(int));
+  w.slots = align(w.kscan + (size_t)kKScanSlots * sizeof(int));
   w.dout = align(w.slots + (size_t)w.pair_heads * 2 * kSplitSlotFloats * sizeof(float));
   w.total = dout_bytes > 0 ? w.dout + dout_bytes : w.slots + (size_t)w.pair_heads * 2 * kSplitSlotFloats * sizeof(float);
   w.dscore = align(w.total);
@@ -420,6 +482,8 @@ hipError_t launch_prologue(const Prologue& pro, hipStream_t stream) {
   for (int i = 0; i < pro.nplan; ++i)
     if (pro.plan[i].cap > 0) a.plan[a.nplan++] = pro.plan[i];
   a.delta = pro.delta;
+  a.kscan = pro.kscan;
+  a.kscan_blocks = pro.has_kscan ? kKScanSlots : 0;
   a.delta_blocks = 0;
   int delta_d = 0;
   if (pro.has_delta && (int64_t)pro.delta.T * pro.delta.Hq > 0) {
@@ -435,7 +499,7 @@ hipError_t launch_prologue(const Prologue& pro, hipStream_t stream) {
       a.fill[a.nfill++] = pro.fill[i];
       a.fill_blocks = (pro.fill[i].T + kFillRows - 1) / kFillRows;  // every target has the same T
     }
-  const int64_t blocks = (int64_t)a.nplan + a.delta_blocks + (int64_t)a.nfill * a.fill_blocks;
+  const int64_t blocks = (int64_t)a.nplan + a.delta_blocks + a.kscan_blocks + (int64_t)a.nfill * a.fill_blocks;
   if (blocks == 0) return hipSuccess;
   const dim3 grid((unsigned)blocks), block(kThreads);
   const bool gated = delta_d > 0 && pro.delta.gate != nullptr;

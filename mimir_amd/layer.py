@@ -105,17 +105,23 @@ class _GatedAttention(torch.autograd.Function):
             q = rope(q, cos, sin)
             k = rope(k, cos, sin)
         y = torch.empty((T, hq, d), dtype=gqkv.dtype, device=gqkv.device)
+        # bf16: the split decision and, when the kernels split, the low half of the
+        # attention output (for the backward's delta row sums)
+        lo = gqkv.dtype == torch.bfloat16
+        out_lo = torch.empty_like(y) if lo else y.new_empty(0)
+        flag = torch.empty(1 if lo else 0, dtype=torch.int32, device=y.device)
         p, out, lse, keep = P.prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
-                                          numseqs, max_seqlen_all, softmax_scale, gate=gate, gated_out=y)
+                                          numseqs, max_seqlen_all, softmax_scale, gate=gate, gated_out=y,
+                                          out_lo=out_lo if lo else None, split_flag=flag)
         _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), P._stream(y.device)))
-        ctx.save_for_backward(gqkv, q, k, out, lse, cos, sin, prefix_lens, causal_lens, cu_seqlens)
+        ctx.save_for_backward(gqkv, q, k, out, lse, out_lo, flag, cos, sin, prefix_lens, causal_lens, cu_seqlens)
         ctx.meta = (hq, hkv, is_causal, total_seqlen, numseqs, max_seqlen_all, softmax_scale)
         return y.reshape(*gqkv.shape[:-1], hq * d)
 
     @staticmethod
     def backward(ctx, dy):
         lib = _capi.load()
-        gqkv, q, k, out, lse, cos, sin, prefix_lens, causal_lens, cu_seqlens = ctx.saved_tensors
+        gqkv, q, k, out, lse, out_lo, flag, cos, sin, prefix_lens, causal_lens, cu_seqlens = ctx.saved_tensors
         hq, hkv, is_causal, total_seqlen, numseqs, max_seqlen_all, softmax_scale = ctx.meta
         T, d, g3, gate, _, _, v = _split(gqkv, hq, hkv)
         dg3 = torch.empty_like(g3)
@@ -123,7 +129,7 @@ class _GatedAttention(torch.autograd.Function):
         dy3 = dy.reshape(T, hq, d)
         p, dq, dk, dv, keep = P.prepare_bwd(dy3, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens,
                                             total_seqlen, numseqs, max_seqlen_all, softmax_scale, gate=gate,
-                                            dgate=dgate, dq=dq, dk=dk, dv=dv)
+                                            dgate=dgate, dq=dq, dk=dk, dv=dv, out_lo=out_lo, split_flag=flag)
         _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd(ctypes.byref(p), P._stream(dg3.device)))
         if cos is not None:
             rope(dq, cos, sin, inverse=True, out=dq)

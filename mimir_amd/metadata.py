@@ -9,6 +9,11 @@ arguments without the reference installed:
 * :class:`PrefixLMSeqInfo` / :func:`prefixlm_seq_info_from_tensors` --
   src/mimir/model/flash_attention_prefixlm_common.py:36-77 (slice padded
   metadata to ``numseqs``; ``cu_seqlens_shifted = cu_seqlens + pad(prefix_lens)``).
+* :func:`prefixlm_prepared_from_tensors` -- src/mimir/model/flash_attention_prefixlm_common.py:87-133,
+  the nine routing tensors that ``prepare_prefixlm_batch`` (src/mimir/model/common.py:36-70)
+  adds to every batch for the ``sm100`` / ``rocm`` backends.  The kernels here
+  take their tiles from ``cu_seqlens`` / ``prefix_lens`` and ignore them; they
+  are restated so that a caller can pass the very keyword set Mimir2 passes.
 * :func:`allowed_pairs` -- the per-sequence count of attended (query, key) pairs,
   ``(n^2 + n + p^2 - p) / 2``, used for the unmasked-FLOP accounting.
 """
@@ -22,11 +27,26 @@ import torch
 from torch import Tensor
 
 __all__ = [
+    "PREFIXLM_ROUTING_KEYS",
     "PrefixLMSeqInfo",
     "allowed_pairs",
     "compute_aux_seq_tensors_scalars",
+    "prefixlm_prepared_from_tensors",
     "prefixlm_seq_info_from_tensors",
 ]
+
+# The keys prepare_prefixlm_batch adds (flash_attention_prefixlm_common.py:124-134).
+PREFIXLM_ROUTING_KEYS = (
+    "prefix_cu_seqlens",
+    "prefix_idx",
+    "causal_idx",
+    "active_key_idx",
+    "active_cu_seqlens_q",
+    "active_cu_seqlens_k",
+    "cu_seqlens_shifted",
+    "prefix_mask",
+    "causal_mask",
+)
 
 
 def compute_aux_seq_tensors_scalars(prefix_lens: np.ndarray, causal_lens: np.ndarray, batch_max_tokens: int):
@@ -104,6 +124,42 @@ def prefixlm_seq_info_from_tensors(
         cu_seqlens=cu,
         cu_seqlens_shifted=shifted,
     )
+
+
+def prefixlm_prepared_from_tensors(prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_prefix,
+                                   max_seqlen_causal, max_seqlen_all) -> dict:
+    """The routing tensors of flash_attention_prefixlm_common.py:87-133 for one packed batch.
+
+    Token t of sequence s at local position i is a prefix token when i < prefix_lens[s];
+    ``prefix_idx`` / ``causal_idx`` list the prefix / causal tokens, ``active_key_idx``
+    the tokens of sequences with a causal part, with their cumulative lengths.
+    Built with device ops from device tensors (``repeat_interleave`` and boolean
+    indexing synchronise once, as in the reference).
+    """
+    info = prefixlm_seq_info_from_tensors(prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+                                          max_seqlen_prefix, max_seqlen_causal, max_seqlen_all)
+    dev = info.prefix_lens.device
+    prefix_cu = torch.nn.functional.pad(torch.cumsum(info.prefix_lens, dim=0, dtype=torch.int32), (1, 0))
+    total_lens = info.prefix_lens + info.causal_lens
+    seq_idx = torch.repeat_interleave(torch.arange(info.numseqs, device=dev), total_lens)
+    valid_idx = torch.arange(info.total_seqlen, device=dev)
+    token_idx = valid_idx - info.cu_seqlens[: info.numseqs][seq_idx]
+    prefix_mask = token_idx < info.prefix_lens[seq_idx]
+    active = info.causal_lens > 0
+    causal_mask = (~prefix_mask) & active[seq_idx]
+    return {
+        "prefix_cu_seqlens": prefix_cu,
+        "prefix_idx": valid_idx[prefix_mask],
+        "causal_idx": valid_idx[causal_mask],
+        "active_key_idx": valid_idx[active[seq_idx]],
+        "active_cu_seqlens_q": torch.nn.functional.pad(
+            torch.cumsum(info.causal_lens[active], dim=0, dtype=torch.int32), (1, 0)),
+        "active_cu_seqlens_k": torch.nn.functional.pad(
+            torch.cumsum(total_lens[active], dim=0, dtype=torch.int32), (1, 0)),
+        "cu_seqlens_shifted": info.cu_seqlens_shifted,
+        "prefix_mask": prefix_mask,
+        "causal_mask": causal_mask,
+    }
 
 
 def allowed_pairs(seq_lens, prefix_lens, is_causal: bool = False) -> int:

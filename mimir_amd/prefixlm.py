@@ -41,6 +41,7 @@ __all__ = [
     "flash_attn_varlen_prefixlm",
     "prefixlm_attn_bwd",
     "prefixlm_attn_fwd",
+    "set_split_mode",
     "set_validate_metadata",
 ]
 
@@ -58,12 +59,16 @@ _validate_metadata = os.environ.get("MIMIR_PREFIXLM_VALIDATE", "0") not in ("", 
 
 
 def set_validate_metadata(enabled: bool) -> None:
-    """Check ``prefix_lens + causal_lens == seq_len`` on every call.
+    """Check ``prefix_lens + causal_lens == seq_len <= max_seqlen_all`` on every call.
 
     The check runs on the device and needs one host synchronisation per call, so
     it is off by default (the FA4 path of the reference does not check either);
-    the reference's dense path raises ``ValueError`` for a mismatch
-    (flash_attention_prefixlm_dense.py:54-55) and so does this one when enabled.
+    the reference's dense path raises ``ValueError`` for a length mismatch
+    (flash_attention_prefixlm_dense.py:54-55) and so does this one when enabled,
+    also for a sequence longer than ``max_seqlen_all``.  Without the check such a
+    sequence is still computed correctly: the tile lists do not depend on
+    ``max_seqlen_all``, and the backward falls back to recomputing dQ when a
+    stored score-gradient tile would not fit its region.
     """
     global _validate_metadata
     _validate_metadata = bool(enabled)
@@ -85,6 +90,28 @@ def set_dscore_workspace_limit(nbytes: int) -> None:
     if nbytes < 0:
         raise ValueError("the limit is a byte count >= 0")
     _dscore_limit_bytes = int(nbytes)
+
+
+_SPLIT_MODES = {"auto": _capi.SPLIT_AUTO, "always": _capi.SPLIT_ALWAYS, "never": _capi.SPLIT_NEVER}
+_split_mode = _SPLIT_MODES[os.environ.get("MIMIR_PREFIXLM_SPLIT", "auto")]
+
+
+def set_split_mode(mode: str) -> None:
+    """Whether the bf16 kernels carry P and dS as two bf16 halves: ``"auto"`` (default), ``"always"``, ``"never"``.
+
+    The bf16 MFMA operands round P (forward O = P V) and dS (backward dQ = dS K,
+    dK = dS^T Q) to 8 significant bits.  dQ and dK are sums of cancelling terms
+    (every row of dS sums to zero) and delta = rowsum(dO * O) inherits O's
+    rounding, so with large key / query entries those roundings dominate the
+    gradients' error.  Split, each operand is hi + lo (one more MFMA per product)
+    and its rounding no longer reaches the result.  ``"auto"`` splits when
+    ``softmax_scale * max|K| > 0.75`` anywhere in the call, decided on the
+    device by the kernels themselves (no host synchronisation).
+    """
+    global _split_mode
+    if mode not in _SPLIT_MODES:
+        raise ValueError(f"split mode must be one of {sorted(_SPLIT_MODES)}, got {mode!r}")
+    _split_mode = _SPLIT_MODES[mode]
 
 
 def _scalar(x) -> int:
@@ -140,36 +167,47 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def check_metadata(prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor, numseqs) -> None:
-    """Raise ``ValueError`` like flash_attention_prefixlm_dense.py:54-55 for a bad sequence.
+def check_metadata(prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor, numseqs,
+                   max_seqlen_all=None) -> None:
+    """Raise ``ValueError`` like flash_attention_prefixlm_dense.py:54-55 for a bad sequence,
+    and for a sequence longer than ``max_seqlen_all`` (when given).
 
     Runs the library's device-side check and synchronises once.
     """
     lib = _capi.load()
     n = _scalar(numseqs)
+    max_all = 0x7FFFFFFF if max_seqlen_all is None else _scalar(max_seqlen_all)
     device = cu_seqlens.device
     _check_device_tensor("cu_seqlens", cu_seqlens)
     pl = _metadata(prefix_lens, device, n, "prefix_lens")
     cl = _metadata(causal_lens, device, n, "causal_lens")
     cu = _metadata(cu_seqlens, device, n + 1, "cu_seqlens")
-    bad = torch.empty(1, dtype=torch.int32, device=device)
-    status = lib.mimir_prefixlm_check_metadata(pl.data_ptr(), cl.data_ptr(), cu.data_ptr(), n, bad.data_ptr(), _stream(device))
+    bad = torch.empty(2, dtype=torch.int32, device=device)
+    status = lib.mimir_prefixlm_check_metadata(pl.data_ptr(), cl.data_ptr(), cu.data_ptr(), n, max_all,
+                                               bad.data_ptr(), _stream(device))
     _capi.raise_for_status(lib, status)
-    s = int(bad.item())
+    s, why = (int(x) for x in bad.tolist())
     if s >= 0:
         p, c = int(pl[s].item()), int(cl[s].item())
         length = int(cu[s + 1].item()) - int(cu[s].item())
+        if why == 2:
+            raise ValueError(f"PrefixLM sequence {s} has length {length} > max_seqlen_all {max_all}")
         raise ValueError(f"Bad PrefixLM lengths for sequence {s}: {p} + {c} != {length}")
 
 
 def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
-                softmax_scale, gate=None, gated_out=None):
+                softmax_scale, gate=None, gated_out=None, out_lo=None, split_mode=None, split_flag=None):
     """Validate, allocate O / lse and fill the C parameter struct of the forward.
 
     Returns ``(params, out, lse, keep)``; ``keep`` holds every tensor the struct
     points to and must outlive the launch.  With ``gate`` ([T, Hq, D], the
     sigmoid output gate of src/mimir/model/layers.py:239) the launch also writes
     ``gated_out`` (same shape; allocated by the caller, may be a strided view).
+    With ``out_lo`` (bf16 [T, Hq, D], caller-allocated) it also writes the low
+    half of the output, round(O - round(O)), which the backward's row sums use.
+    ``split_mode`` is a ``_capi.SPLIT_*`` mode (default: :func:`set_split_mode`);
+    with ``split_flag`` (int32 [1], caller-allocated) the launch records its split
+    decision there and writes ``out_lo`` only when it splits.
     """
     for name, t in (("q", q), ("k", k), ("v", v)):
         _check_device_tensor(name, t)
@@ -179,12 +217,12 @@ def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_
     pl = _metadata(prefix_lens, device, n, "prefix_lens")
     cl = _metadata(causal_lens, device, n, "causal_lens")
     cu = _metadata(cu_seqlens, device, n + 1, "cu_seqlens")
+    max_all = _scalar(max_seqlen_all)
     if _validate_metadata:
-        check_metadata(pl, cl, cu, n)
+        check_metadata(pl, cl, cu, n, max_all)
     q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
     out = torch.empty((T, hq, d), dtype=q.dtype, device=device)
     lse = torch.empty((hq, T), dtype=torch.float32, device=device)
-    max_all = _scalar(max_seqlen_all)
     ws_bytes = int(_capi.load().mimir_prefixlm_fwd_workspace_bytes(T, n, max_all))
     ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
     p = _capi.FwdParams(
@@ -195,7 +233,11 @@ def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_
         T, hq, hkv, d, n, _scalar(total_seqlen), max_all, int(bool(is_causal)),
         _DTYPES[q.dtype], float(softmax_scale), ws.data_ptr(), ws_bytes,
     )
+    p.split_mode = _split_mode if split_mode is None else int(split_mode)
     keep = (q, k, v, pl, cl, cu, ws)
+    if split_flag is not None and split_flag.numel() > 0:
+        p.split_flag = split_flag.data_ptr()
+        keep = keep + (split_flag,)
     if gate is not None:
         gate = _gate_operand("gate", gate, (T, hq, d), q.dtype)
         _gate_operand("gated_out", gated_out, (T, hq, d), q.dtype, copy=False)
@@ -203,6 +245,10 @@ def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_
         p.gated_out = gated_out.data_ptr()
         p.gated_out_stride_token, p.gated_out_stride_head = gated_out.stride(0), gated_out.stride(1)
         keep = keep + (gate, gated_out)
+    if out_lo is not None:
+        _gate_operand("out_lo", out_lo, (T, hq, d), q.dtype, copy=False)
+        p.out_lo, p.out_lo_stride_token, p.out_lo_stride_head = out_lo.data_ptr(), out_lo.stride(0), out_lo.stride(1)
+        keep = keep + (out_lo,)
     return p, out, lse, keep
 
 
@@ -223,23 +269,42 @@ def _gate_operand(name: str, t, shape, dtype, copy: bool = True) -> Tensor:
     return laid
 
 
+def _wants_lo(q: Tensor) -> bool:
+    return q.dtype == torch.bfloat16
+
+
 def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
               softmax_scale):
     lib = _capi.load()
+    # bf16: the split decision and, when it splits, the output's low half (for the
+    # backward's delta = rowsum(dO * O)); float32 needs neither
+    lo = _wants_lo(q)
+    out_lo = torch.empty(q.shape, dtype=q.dtype, device=q.device) if lo else q.new_empty(0)
+    flag = torch.empty(1 if lo else 0, dtype=torch.int32, device=q.device)
     p, out, lse, keep = prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
-                                    numseqs, max_seqlen_all, softmax_scale)
+                                    numseqs, max_seqlen_all, softmax_scale, out_lo=out_lo if lo else None,
+                                    split_flag=flag)
     _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), _stream(out.device)))
-    return out, lse
+    return out, lse, out_lo, flag
 
 
 def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-                max_seqlen_all, softmax_scale, gate=None, dgate=None, dq=None, dk=None, dv=None):
+                max_seqlen_all, softmax_scale, gate=None, dgate=None, dq=None, dk=None, dv=None, out_lo=None,
+                split_mode=None, split_flag=None):
     """Validate, allocate dQ / dK / dV and the workspace, fill the backward struct.
 
     Returns ``(params, dq, dk, dv, keep)``.  With ``gate``, ``dout`` is the
     gradient of the gated output and ``out`` the ungated attention output; the
     launch writes ``dgate`` (caller-allocated).  ``dq`` / ``dk`` / ``dv`` may be
     given as (strided) output views, e.g. slices of a fused gqkv gradient.
+    ``out_lo`` is the forward's low output half (bf16), ``split_mode`` a
+    ``_capi.SPLIT_*`` mode (default: :func:`set_split_mode`), ``split_flag`` the
+    forward's recorded split decision (then followed instead of scanning K).
+
+    The workspace holds the score-gradient hand-off region when it fits the
+    limit (:func:`set_dscore_workspace_limit`); if that allocation runs out of
+    device memory the backward falls back to recomputing dQ with the small
+    workspace instead of failing.
     """
     lib = _capi.load()
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout)):
@@ -280,18 +345,35 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
     if gate is not None:
         p.gate, p.gate_stride_token, p.gate_stride_head = gate.data_ptr(), gate.stride(0), gate.stride(1)
         p.dgate, p.dgate_stride_token, p.dgate_stride_head = dgate.data_ptr(), dgate.stride(0), dgate.stride(1)
+    if out_lo is not None and out_lo.numel() > 0:
+        out_lo = _gate_operand("out_lo", out_lo, (T, hq, d), q.dtype)
+        p.out_lo, p.out_lo_stride_token, p.out_lo_stride_head = out_lo.data_ptr(), out_lo.stride(0), out_lo.stride(1)
+        gate_keep = gate_keep + (out_lo,)
+    p.split_mode = _split_mode if split_mode is None else int(split_mode)
+    if split_flag is not None and split_flag.numel() > 0:
+        p.split_flag = split_flag.data_ptr()
+        gate_keep = gate_keep + (split_flag,)
     p.dscore_limit_bytes = _dscore_limit_bytes
     ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p)))
-    ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
+    try:
+        ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
+    except torch.cuda.OutOfMemoryError:
+        if int(lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p))) == 0:
+            raise
+        # no room for the score-gradient tiles: the recomputing dQ needs none
+        p.dscore_limit_bytes = 0
+        ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p)))
+        ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
     p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
     return p, dq, dk, dv, (q, k, v, out, dout, lse, pl, cl, cu, ws) + gate_keep
 
 
-def _bwd_impl(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-              max_seqlen_all, softmax_scale):
+def _bwd_impl(dout, q, k, v, out, lse, out_lo, split_flag, is_causal, prefix_lens, causal_lens, cu_seqlens,
+              total_seqlen, numseqs, max_seqlen_all, softmax_scale):
     lib = _capi.load()
     p, dq, dk, dv, keep = prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens,
-                                      total_seqlen, numseqs, max_seqlen_all, softmax_scale)
+                                      total_seqlen, numseqs, max_seqlen_all, softmax_scale, out_lo=out_lo,
+                                      split_flag=split_flag)
     _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd(ctypes.byref(p), _stream(dq.device)))
     return dq, dk, dv
 
@@ -301,7 +383,9 @@ def _prefixlm_fwd_op(
     q: Tensor, k: Tensor, v: Tensor, is_causal: bool,
     prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
     total_seqlen: Tensor, numseqs: Tensor, max_seqlen_all: Tensor, softmax_scale: float,
-) -> tuple[Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(O, lse, O_lo, split_flag): for bf16 the low output half (written only when the
+    kernels split P) and the recorded split decision; both empty for float32."""
     return _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
                      max_seqlen_all, softmax_scale)
 
@@ -309,23 +393,28 @@ def _prefixlm_fwd_op(
 @_prefixlm_fwd_op.register_fake
 def _(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
       softmax_scale):
-    return torch.empty_like(q, memory_format=torch.contiguous_format), q.new_empty(
-        (q.shape[1], q.shape[0]), dtype=torch.float32)
+    cf = torch.contiguous_format
+    lo = torch.empty_like(q, memory_format=cf) if _wants_lo(q) else q.new_empty(0)
+    flag = q.new_empty(1 if _wants_lo(q) else 0, dtype=torch.int32)
+    return (torch.empty_like(q, memory_format=cf), q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32), lo,
+            flag)
 
 
 @torch.library.custom_op("mimir_amd::prefixlm_bwd", mutates_args=())
 def _prefixlm_bwd_op(
-    dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor, is_causal: bool,
-    prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
+    dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor, out_lo: Tensor, split_flag: Tensor,
+    is_causal: bool, prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
     total_seqlen: Tensor, numseqs: Tensor, max_seqlen_all: Tensor, softmax_scale: float,
 ) -> tuple[Tensor, Tensor, Tensor]:
-    return _bwd_impl(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
-                     numseqs, max_seqlen_all, softmax_scale)
+    """(dQ, dK, dV); an empty ``out_lo`` means delta from ``out`` alone, an empty
+    ``split_flag`` that the backward makes its own split decision."""
+    return _bwd_impl(dout, q, k, v, out, lse, out_lo, split_flag, is_causal, prefix_lens, causal_lens, cu_seqlens,
+                     total_seqlen, numseqs, max_seqlen_all, softmax_scale)
 
 
 @_prefixlm_bwd_op.register_fake
-def _(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-      max_seqlen_all, softmax_scale):
+def _(dout, q, k, v, out, lse, out_lo, split_flag, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
+      numseqs, max_seqlen_all, softmax_scale):
     cf = torch.contiguous_format
     return (torch.empty_like(q, memory_format=cf), torch.empty_like(k, memory_format=cf),
             torch.empty_like(v, memory_format=cf))
@@ -343,10 +432,10 @@ class PrefixLMAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
                 max_seqlen_all, softmax_scale):
-        out, lse = _prefixlm_fwd_op(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
-                                    numseqs, max_seqlen_all, softmax_scale)
-        ctx.save_for_backward(q, k, v, out, lse, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
-                              max_seqlen_all)
+        out, lse, out_lo, flag = _prefixlm_fwd_op(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
+                                                  total_seqlen, numseqs, max_seqlen_all, softmax_scale)
+        ctx.save_for_backward(q, k, v, out, lse, out_lo, flag, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
+                              numseqs, max_seqlen_all)
         ctx.mark_non_differentiable(lse)
         ctx.is_causal = bool(is_causal)
         ctx.softmax_scale = float(softmax_scale)
@@ -354,12 +443,13 @@ class PrefixLMAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, dlse):
-        (q, k, v, out, lse, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
+        (q, k, v, out, lse, out_lo, flag, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
          max_seqlen_all) = ctx.saved_tensors
         if dout is None:
             dout = torch.zeros_like(out)
-        dq, dk, dv = _prefixlm_bwd_op(dout, q, k, v, out, lse, ctx.is_causal, prefix_lens, causal_lens,
-                                      cu_seqlens, total_seqlen, numseqs, max_seqlen_all, ctx.softmax_scale)
+        dq, dk, dv = _prefixlm_bwd_op(dout, q, k, v, out, lse, out_lo, flag, ctx.is_causal, prefix_lens,
+                                      causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
+                                      ctx.softmax_scale)
         return dq, dk, dv, None, None, None, None, None, None, None, None
 
 
@@ -384,12 +474,18 @@ def prefixlm_attn_fwd(
 def prefixlm_attn_bwd(
     dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor, is_causal: bool,
     prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
-    total_seqlen, numseqs, max_seqlen_all, softmax_scale: Optional[float] = None,
+    total_seqlen, numseqs, max_seqlen_all, softmax_scale: Optional[float] = None, out_lo: Optional[Tensor] = None,
+    split_flag: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor]:
-    """Explicit backward: ``(dQ, dK, dV)`` from ``dO``, ``O`` and ``lse``."""
+    """Explicit backward: ``(dQ, dK, dV)`` from ``dO``, ``O`` and ``lse``.  For bf16, optionally the
+    forward's low output half ``out_lo`` (delta = rowsum(dO * O) then exact to ~2^-17) and its
+    recorded ``split_flag`` (the low half is then read only when the forward split)."""
     scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else float(softmax_scale)
-    return _prefixlm_bwd_op(dout, q, k, v, out, lse, bool(is_causal), prefix_lens, causal_lens, cu_seqlens,
-                            _cpu_scalar(total_seqlen), _cpu_scalar(numseqs), _cpu_scalar(max_seqlen_all), scale)
+    lo = q.new_empty(0) if out_lo is None else out_lo
+    flag = q.new_empty(0, dtype=torch.int32) if split_flag is None else split_flag
+    return _prefixlm_bwd_op(dout, q, k, v, out, lse, lo, flag, bool(is_causal), prefix_lens, causal_lens,
+                            cu_seqlens, _cpu_scalar(total_seqlen), _cpu_scalar(numseqs),
+                            _cpu_scalar(max_seqlen_all), scale)
 
 
 def flash_attn_varlen_prefixlm(

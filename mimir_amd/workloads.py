@@ -1,6 +1,6 @@
 """Seeded synthetic prefix-LM workloads and their work accounting.
 
-The five measured shapes are the Mimir2 prefix-LM attention workloads:
+The six measured shapes are the Mimir2 prefix-LM attention workloads:
 
 1. fp32 forward, 4 x 512 tokens, 8 q-heads = 8 kv-heads, head_dim 64, prefix ~ U{0..512}
 2. bf16 fwd+bwd, 8 x 2048 tokens, 16 q-heads / 4 kv-heads (GQA 4:1), head_dim 128, prefix ~ U{0..2048}
@@ -9,6 +9,11 @@ The five measured shapes are the Mimir2 prefix-LM attention workloads:
 4. bf16 fwd+bwd, 1 x 32768 tokens, 32 / 8 heads, head_dim 128, prefix 8192, one
    head_dim channel of q and k scaled x20 (softmax stress)
 5. bf16 fwd+bwd, 64 x 1024 tokens, 8 / 8 heads, head_dim 64, prefix in {0, 1024}
+6. bf16 fwd+bwd, the shape Mimir2's packaged sizes train at: multi-head attention
+   (num_key_value_heads = num_heads, src/mimir/model/transformer.py:78) with the XXS
+   size's 2 heads of 128 (src/mimir/conf/size/XXS.yaml:4-5, hidden 256), one packed row
+   of 24576 tokens (global_batch_size 196608 / 8 ranks, src/mimir/conf/train.yaml:10)
+   split into documents like workload 3 (the data config fixes no length law)
 
 Inputs are drawn from a CPU ``torch.Generator`` in a fixed order -- q, k, v, dO
 (standard normal, fp32) and then the metadata -- and cast to the compute dtype.
@@ -40,6 +45,7 @@ CONFIG_NAMES = {
     3: "packed_docs_bf16_t16384_hq16_hkv4_d128",
     4: "longctx_bf16_s32768_hq32_hkv8_d128_p8192_outlier20",
     5: "smallhead_bf16_b64_s1024_h8_d64_p0or1024",
+    6: "xxs_mha_bf16_t24576_h2_d128_packed_docs",
 }
 
 
@@ -152,7 +158,7 @@ def make_case(seq_lens, prefixes, hq: int, hkv: int, d: int, *, seed: int = 0, d
 
 
 def make_config(idx: int, seed: int = 0, dtype=None) -> Case:
-    """One of the five measured workloads (see module docstring)."""
+    """One of the six measured workloads (see module docstring)."""
     gen = torch.Generator().manual_seed(seed)
     if idx == 1:
         T, hq, hkv, d, dt = 2048, 8, 8, 64, torch.float32
@@ -162,6 +168,8 @@ def make_config(idx: int, seed: int = 0, dtype=None) -> Case:
         T, hq, hkv, d, dt = 32768, 32, 8, 128, torch.bfloat16
     elif idx == 5:
         T, hq, hkv, d, dt = 65536, 8, 8, 64, torch.bfloat16
+    elif idx == 6:
+        T, hq, hkv, d, dt = 24576, 2, 2, 128, torch.bfloat16
     else:
         raise ValueError(f"unknown workload {idx}")
     dt = dtype or dt
@@ -172,7 +180,7 @@ def make_config(idx: int, seed: int = 0, dtype=None) -> Case:
     elif idx == 2:
         seq_lens = [2048] * 8
         prefixes = torch.randint(0, 2049, (8,), generator=gen).tolist()
-    elif idx == 3:
+    elif idx in (3, 6):
         seq_lens, prefixes, left = [], [], T
         while left > 0:
             L = int(torch.randint(128, 4097, (1,), generator=gen).item())

@@ -24,7 +24,16 @@ function                        pinned by
 ``dense_lse``                   brute force; logsumexp of a single allowed key
 ``dense_backward``              torch.autograd of ``dense_forward`` in fp64,
                                 ``torch.autograd.gradcheck``, brute-force loops
+``chunked_forward_backward``    equality with ``dense_forward`` / ``dense_lse`` /
+                                ``dense_backward`` (chunked == unchunked, every
+                                chunk size, GQA, padding rows, is_causal)
 =============================  ===================================================
+
+``chunked_forward_backward`` evaluates the same closed forms query-chunk by
+query-chunk and head by head, so a 32k-token sequence never needs more than a
+chunk x n score matrix; it takes any floating dtype and device (the long-context
+parity test runs it in float64 on the GPU through torch's own matmul, not
+through anything of the product).
 """
 
 from __future__ import annotations
@@ -39,6 +48,7 @@ __all__ = [
     "allowed",
     "brute_force_backward",
     "brute_force_forward",
+    "chunked_forward_backward",
     "dense_backward",
     "dense_forward",
     "dense_forward_autograd",
@@ -221,6 +231,60 @@ def dense_backward(q, k, v, out, dout, is_causal, prefix_lens, causal_lens, cu_s
         dk[start:end] = dk_rep.reshape(hkv, rep, n, d).sum(1).transpose(0, 1)
         dv[start:end] = dv_rep.reshape(hkv, rep, n, d).sum(1).transpose(0, 1)
     return dq, dk, dv
+
+
+def chunked_forward_backward(q, k, v, dout, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
+                             numseqs, scale: float | None = None, chunk: int = 4096):
+    """O, lse, dQ, dK, dV of the reference's masked attention from (q, k, v, dO) alone.
+
+    The closed forms of :func:`dense_forward`, :func:`dense_lse` and
+    :func:`dense_backward` (flash_attention_prefixlm_dense.py:19-81 and the
+    backward of flash_attention_prefixlm_mps.py:1601-1675 with the GQA sum of
+    dense.py:10-16), evaluated per sequence, q head and block of ``chunk`` query
+    rows: S = scale Q K^T over the keys the block can see, P = exp(S - lse),
+    O = P V, delta = rowsum(dO * O) from this O, dS = P (dO V^T - delta) * scale,
+    dQ = dS K, dK += dS^T Q, dV += P^T dO.  Rows at or after ``total_seqlen`` get
+    O = 0, lse = -inf and no gradient (dense.py:79-80).  Works in the dtype and on
+    the device of the inputs.
+    """
+    T, hq, d = q.shape
+    hkv = k.shape[1]
+    rep = hq // hkv
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    total = int(total_seqlen)
+    out = torch.zeros_like(q)
+    lse = torch.full((hq, T), float("-inf"), dtype=q.dtype, device=q.device)
+    dq = torch.zeros_like(q)
+    dk = torch.zeros_like(k)
+    dv = torch.zeros_like(v)
+    for start, end, p in _seqs(prefix_lens, causal_lens, cu_seqlens, numseqs):
+        n = end - start
+        nq = max(0, min(n, total - start))
+        pos = torch.arange(n, device=q.device)
+        for h in range(hq):
+            g = h // rep
+            ks, vs = k[start:end, g], v[start:end, g]                      # [n, d]
+            for a in range(0, nq, chunk):
+                b = min(nq, a + chunk)
+                kend = b if is_causal else max(p, b)                        # keys any row of the block sees
+                qs, dos = q[start + a:start + b, h], dout[start + a:start + b, h]
+                kc, vc = ks[:kend], vs[:kend]
+                sc = torch.matmul(qs, kc.transpose(0, 1).contiguous()) * scale
+                rows = pos[a:b, None]
+                cols = pos[None, :kend]
+                allowed = cols <= rows if is_causal else (cols < torch.clamp(rows + 1, min=p))
+                sc = sc.masked_fill(~allowed, float("-inf"))
+                l_ = torch.logsumexp(sc, dim=1)
+                pr = torch.exp(sc - l_[:, None])
+                o = torch.matmul(pr, vc)
+                delta = (dos * o).sum(dim=1, keepdim=True)
+                ds = pr * (torch.matmul(dos, vc.transpose(0, 1).contiguous()) - delta) * scale
+                out[start + a:start + b, h] = o
+                lse[h, start + a:start + b] = l_
+                dq[start + a:start + b, h] = torch.matmul(ds, kc)
+                dk[start:start + kend, g] += torch.matmul(ds.transpose(0, 1).contiguous(), qs)
+                dv[start:start + kend, g] += torch.matmul(pr.transpose(0, 1).contiguous(), dos)
+    return out, lse, dq, dk, dv
 
 
 # ---------------------------------------------------------------------------

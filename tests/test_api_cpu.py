@@ -77,12 +77,42 @@ def test_signature_matches_reference_keywords():
 def test_custom_ops_registered_with_fake_kernels():
     assert hasattr(torch.ops.mimir_amd, "prefixlm_fwd") and hasattr(torch.ops.mimir_amd, "prefixlm_bwd")
     c = make_case([6, 10], [2, 10], 4, 2, 64, dtype=torch.bfloat16)
+    meta = (c.prefix_lens, c.causal_lens, c.cu_seqlens, c.total_seqlen, c.numseqs, c.max_seqlen_all, 0.125)
     with torch._subclasses.fake_tensor.FakeTensorMode(allow_non_fake_inputs=True):
         q = torch.empty(16, 4, 64, dtype=torch.bfloat16)
         k = torch.empty(16, 2, 64, dtype=torch.bfloat16)
-        out, lse = torch.ops.mimir_amd.prefixlm_fwd(q, k, k, False, c.prefix_lens, c.causal_lens, c.cu_seqlens,
-                                                    c.total_seqlen, c.numseqs, c.max_seqlen_all, 0.125)
+        out, lse, lo, flag = torch.ops.mimir_amd.prefixlm_fwd(q, k, k, False, *meta)
         assert out.shape == (16, 4, 64) and lse.shape == (4, 16) and lse.dtype == torch.float32
+        assert lo.shape == out.shape and lo.dtype == torch.bfloat16
+        assert flag.shape == (1,) and flag.dtype == torch.int32
+        dq, dk, dv = torch.ops.mimir_amd.prefixlm_bwd(out, q, k, k, out, lse, lo, flag, False, *meta)
+        assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape and dk.dtype == torch.bfloat16
+        qf = torch.empty(16, 4, 64)
+        kf = torch.empty(16, 2, 64)
+        out, lse, lo, flag = torch.ops.mimir_amd.prefixlm_fwd(qf, kf, kf, False, *meta)
+        assert lo.numel() == 0 and flag.numel() == 0  # float32 carries no low half and no split
+
+
+def test_forward_and_backward_trace_with_fake_tensors():
+    """The drop-in with autograd traced by make_fx in fake mode: forward and backward become
+    exactly one call each of the two custom ops, shaped by their fake kernels alone (no device
+    work, no data-dependent host reads), as torch.compile would see them."""
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    c = make_case([6, 10], [2, 10], 4, 2, 64, dtype=torch.bfloat16)
+
+    def step(q, k, v, dout, *meta):
+        out = flash_attn_varlen_prefixlm(q, k, v, False, *meta)
+        return torch.autograd.grad(out, (q, k, v), dout)
+
+    args = (torch.randn(16, 4, 64, dtype=torch.bfloat16, requires_grad=True),
+            torch.randn(16, 2, 64, dtype=torch.bfloat16, requires_grad=True),
+            torch.randn(16, 2, 64, dtype=torch.bfloat16, requires_grad=True),
+            torch.randn(16, 4, 64, dtype=torch.bfloat16)) + c.call_args()
+    gm = make_fx(step, tracing_mode="fake")(*args)
+    targets = [str(n.target) for n in gm.graph.nodes if n.op == "call_function"]
+    assert sum("mimir_amd.prefixlm_fwd" in t for t in targets) == 1, targets
+    assert sum("mimir_amd.prefixlm_bwd" in t for t in targets) == 1, targets
 
 
 @pytest.mark.parametrize("idx", [1, 2, 3])

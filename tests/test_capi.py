@@ -49,10 +49,16 @@ def test_abi_version(lib):
     assert lib.mimir_prefixlm_abi_version() == _capi.ABI_VERSION
 
 
+def _fwd_workspace(T, numseqs):
+    """Forward workspace: the tile list, one int32 pair per entry, ceil(T / 128) + numseqs entries
+    (max_seqlen_all unused), then 256-byte aligned the 512 int32 K-scan slots."""
+    cap = -(-T // 128) + numseqs
+    return (cap * 8 + 255) // 256 * 256 + 512 * 4
+
+
 def test_workspace_bytes(lib):
-    # tile lists: one int32 pair per 128-row tile, min(numseqs * ceil(max_len / 128), ceil(T / 128) + numseqs)
-    assert lib.mimir_prefixlm_fwd_workspace_bytes(16384, 8, 2048) == 8 * 16 * 8
-    assert lib.mimir_prefixlm_fwd_workspace_bytes(16384, 1000, 4096) == (128 + 1000) * 8
+    for T, ns, mx in ((16384, 8, 2048), (16384, 8, 100), (16384, 1000, 4096), (5, 1, 5)):
+        assert lib.mimir_prefixlm_fwd_workspace_bytes(T, ns, mx) == _fwd_workspace(T, ns), (T, ns, mx)
     assert lib.mimir_prefixlm_fwd_workspace_bytes(0, 8, 2048) == 0
     for args in ((16384, 16, 8, 2048), (2048, 8, 4, 512), (16384, 16, 1000, 4096), (100, 3, 1, 100)):
         assert lib.mimir_prefixlm_bwd_workspace_bytes(*args) == _bwd_workspace(*args), args
@@ -62,18 +68,43 @@ def test_workspace_bytes(lib):
 def _bwd_workspace(T, hq, numseqs, max_len):
     """Backward workspace: 256-byte aligned sections delta and lse*log2(e) (float32 [Hq, T]), the
     query-tile list (int2 per tile), the key-tile list (int4 per tile plus one per possible split pair),
-    one int32 counter per split (pair, kv head) plus two work-queue counters, and two float32 slots of
-    2 * 128 * 128 per split (pair, kv head)."""
+    one int32 counter per split (pair, kv head) plus two work-queue counters and the dS-incomplete flag,
+    512 int32 K-scan slots, and two float32 slots of 2 * 128 * 128 per split (pair, kv head)."""
     def align(x):
         return (x + 255) // 256 * 256
-    cap = min(numseqs * -(-max_len // 128), -(-T // 128) + numseqs)
+    cap = -(-T // 128) + numseqs
     pair_heads = min(384, cap * hq)
     lse2 = align(T * hq * 4)
     plan_q = align(lse2 + T * hq * 4)
     plan_k = align(plan_q + cap * 8)
     counters = align(plan_k + (cap + pair_heads) * 16)
-    slots = align(counters + (pair_heads + 2) * 4)
+    kscan = align(counters + (pair_heads + 3) * 4)
+    slots = align(kscan + 512 * 4)
     return slots + pair_heads * 2 * 2 * 128 * 128 * 4
+
+
+def test_tile_list_capacity_covers_every_packing(lib):
+    """The list capacity ceil(T / 128) + numseqs bounds sum_s ceil(n_s / 128) for every packing of at
+    most T tokens into numseqs sequences, whatever max_seqlen_all says: random packings, all-equal,
+    one long sequence plus empties, and lengths of 128 k + 1 (the worst case of the ceilings)."""
+    import numpy as np
+
+    rng = np.random.default_rng(0)
+    packings = [[128 * 3 + 1] * 40, [16384] + [0] * 7, [1] * 300, [2048] * 8, [129] * 100]
+    for _ in range(200):
+        ns = int(rng.integers(1, 60))
+        cuts = np.sort(rng.integers(0, 20000, ns - 1))
+        packings.append(np.diff(np.concatenate([[0], cuts, [int(rng.integers(cuts[-1] if ns > 1 else 0, 20001))]]))
+                        .tolist())
+    for lens in packings:
+        T, ns = int(sum(lens)) + int(rng.integers(0, 200)), len(lens)
+        if T == 0:
+            continue
+        tiles = sum(-(-n // 128) for n in lens)
+        cap = -(-T // 128) + ns
+        assert tiles <= cap, (lens[:5], T, ns, tiles, cap)
+        for claimed_max in (1, max(lens) if max(lens) > 0 else 1):  # an understated max changes nothing
+            assert lib.mimir_prefixlm_fwd_workspace_bytes(T, ns, claimed_max) == _fwd_workspace(T, ns)
 
 
 def _c_layout(struct_name, fields):
@@ -164,10 +195,39 @@ def test_dscore_workspace_bytes(lib):
         assert lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)) == got
         size = lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p))
         assert size == (base if got == 0 else ((base + 255) // 256) * 256 + expect)
+    p.split_mode = _capi.SPLIT_ALWAYS  # the stored tiles have no low half: no hand-off
+    assert lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)) == 0
+    p.split_mode = _capi.SPLIT_NEVER
+    assert lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)) == expect
+    p.split_mode = _capi.SPLIT_AUTO
     p.head_dim = 64
     assert lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)) == 0
     p.head_dim, p.dtype = 128, _capi.DTYPE_FLOAT32
     assert lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)) == 0
+
+
+def test_low_half_and_split_mode_validation(lib):
+    """out_lo is a bf16-only operand (forward and backward); split_mode must be a known mode.
+    Both are rejected before any launch (the tensors here are NULL / fake addresses)."""
+    p = _fwd(dtype=_capi.DTYPE_FLOAT32, q=16, k=16, v=16, out=16, q_stride_token=512, q_stride_head=128,
+             k_stride_token=256, k_stride_head=128, v_stride_token=256, v_stride_head=128, out_stride_token=512,
+             out_stride_head=128, prefix_lens=16, cu_seqlens=16, workspace=16, workspace_bytes=1 << 20,
+             out_lo=16, out_lo_stride_token=512, out_lo_stride_head=128)
+    assert lib.mimir_prefixlm_fwd(ctypes.byref(p), None) == _capi.ERR_INVALID_ARGUMENT
+    assert b"out_lo" in lib.mimir_prefixlm_last_error()
+    b = _capi.BwdParams()
+    for f, v in dict(total_tokens=16, num_q_heads=4, num_kv_heads=2, head_dim=128, numseqs=1, total_seqlen=16,
+                     max_seqlen_all=16, dtype=_capi.DTYPE_BFLOAT16, softmax_scale=0.088, lse_stride_head=16,
+                     prefix_lens=16, cu_seqlens=16, lse=16).items():
+        setattr(b, f, v)
+    for name in ("q", "k", "v", "out", "dout", "dq", "dk", "dv"):
+        heads = 4 if name in ("q", "out", "dout", "dq") else 2
+        setattr(b, name, 16)
+        setattr(b, name + "_stride_token", heads * 128)
+        setattr(b, name + "_stride_head", 128)
+    b.split_mode = 3
+    assert lib.mimir_prefixlm_bwd(ctypes.byref(b), None) == _capi.ERR_INVALID_ARGUMENT
+    assert b"split_mode" in lib.mimir_prefixlm_last_error()
 
 
 def test_unknown_backward_stage_bits(lib):

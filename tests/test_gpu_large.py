@@ -1,30 +1,32 @@
 """GPU checks at the full measured sizes.
 
-The oracle cannot evaluate a 32768-token sequence in a test's time budget, so the
-long-context workload is checked on a seeded sample of query rows (O, lse and dQ
-from the closed form restricted to those rows, all keys) plus size-independent
-invariants that hold for every workload.
+The long-context workload (one sequence of 32768 tokens, prefix 8192, Hq 32 / Hkv 8,
+head_dim 128, one q / k channel scaled x20) is compared in full -- every element of
+O, lse, dQ, dK and dV -- with the oracle's closed forms evaluated in float64
+(``chunked_forward_backward``: the dense path of flash_attention_prefixlm_dense.py:19-81
+and the backward of flash_attention_prefixlm_mps.py:1601-1675, query block by query
+block).  At this size the fp64 evaluation runs on the GPU through torch's own
+matmul; a seeded sample of rows is also evaluated on the CPU, which pins that GPU
+evaluation to the CPU oracle.
 
-dQ of the long-context workload (one q/k channel scaled x20, near one-hot softmax
-rows) is compared with the closed form evaluated on the operands a flash backward
-receives and multiplies: the saved lse and bf16 O (delta = rowsum(dO * O)), and dS
-rounded to bf16 before the dS K product (the reference's FA4 wrapper does the
-same). Near one-hot rows amplify a 2e-4 lse difference, which fp32 accumulation
-of |S| ~ 300 logits can leave, into ~0.2 of dQ on the x20 channel, so the saved
-lse is the operand to compare against. On these
-rows those two roundings alone move dQ by 0.44 from the all-fp32 closed form
-(0.40 from O, 0.19 from dS), so the all-fp32 comparison is reported and bounded by
-1.5 x that emulated shift plus 5e-2, while the operand-matched comparison keeps 5e-2.
+Tolerances (max-abs): O 2e-2, lse 1e-2; dQ / dK / dV 5e-2 per channel, or two bf16
+half-ulps of that channel's max|ref| where the output's own bf16 resolution is
+coarser.  On this workload it is: with the x20 channel some keys draw most of the
+attention of thousands of queries, and max|dK| reaches ~800 and max|dV| ~550 (one
+bf16 half-ulp there is 2.0), max|dQ| ~50 (half-ulp 0.125); storing the exact result
+in bf16 already moves it by up to a half-ulp.  The x20 channel also makes dQ and
+dK differences of large terms (in each softmax row sum_j dS_ij = 0), so the bf16
+rounding of P in O = P V (which delta = rowsum(dO * O) inherits) and of dS in
+dQ = dS K and dK = dS^T Q is amplified by max|K| / |dQ|; unsplit these give dQ and
+dK errors of ~8 half-ulps.  The kernels carry P and dS as bf16 hi + lo when
+softmax_scale * max|K| > 0.75 (this workload) and write O's low half for delta.
 
-Invariants:
+Invariants (every bf16 workload):
 
 * sum over the keys of a sequence of dK is zero: dK = scale * dS^T Q and every
   row of dS sums to zero (sum_j P_ij (dP_ij - delta_i) = 0);
 * sum over the keys of a sequence of dV equals the sum over the sequence's
   active queries of dO, summed over the q-heads of each kv head (rows of P sum to 1).
-
-Tolerances (max-abs): O 2e-2, dQ 5e-2, lse 1e-2; invariants relative to the
-magnitude of the summed terms.
 """
 
 import math
@@ -32,9 +34,10 @@ import math
 import pytest
 import torch
 
+from mimir_amd import prefixlm as P
 from mimir_amd import prefixlm_attn_fwd
-from mimir_amd.workloads import make_config
-from oracle.prefixlm_oracle import prefixlm_mask
+from mimir_amd.workloads import make_case, make_config
+from oracle.prefixlm_oracle import chunked_forward_backward, prefixlm_mask
 
 pytestmark = pytest.mark.gpu
 
@@ -74,46 +77,108 @@ def test_gradient_invariants(device, idx):
     check_invariants(case, dk, dv, f"cfg{idx}")
 
 
-def test_long_context_sampled_rows(device):
+def half_ulp_bf16(x: torch.Tensor) -> torch.Tensor:
+    """Half the bf16 spacing at |x| (8 significant bits)."""
+    return torch.exp2(torch.floor(torch.log2(x.abs().clamp_min(1e-30))) - 8)
+
+
+def report(name, got, ref, tol, channel_dim=True):
+    """Max-abs error, and per channel its ratio to the bf16 half-ulp of that channel's max|ref|."""
+    err = (got.double() - ref).abs()
+    worst = err.max().item()
+    line = f"{name} max-abs {worst:.4g} (tol {tol:g})"
+    if channel_dim:
+        e_ch = err.reshape(-1, err.shape[-1]).max(0).values
+        r_ch = ref.abs().reshape(-1, ref.shape[-1]).max(0).values
+        c = int(e_ch.argmax())
+        line += (f"; worst channel {c}: max|ref| {r_ch[c].item():.4g}, bf16 half-ulp {half_ulp_bf16(r_ch[c]).item():.3g},"
+                 f" error = {(e_ch[c] / half_ulp_bf16(r_ch[c])).item():.2f} half-ulps")
+    print(f"[cfg4 full] {line}", flush=True)
+    return worst
+
+
+def channel_excess(got, ref):
+    """Per channel (last dim): max-abs error / max(5e-2, 2 bf16 half-ulps of the channel's max|ref|)."""
+    e_ch = (got.double() - ref).abs().reshape(-1, ref.shape[-1]).max(0).values
+    bound = torch.clamp(2 * half_ulp_bf16(ref.abs().reshape(-1, ref.shape[-1]).max(0).values), min=5e-2)
+    return e_ch / bound
+
+
+def assert_channel_bound(name, got, ref):
+    ratio = channel_excess(got, ref)
+    worst = int(ratio.argmax())
+    assert (ratio <= 1).all(), (name, worst, ratio[worst].item())
+
+
+def test_long_context_full_fp64_reference(device):
     case = make_config(4, seed=0)
     out, lse, dq, dk, dv = run(case, device)
     check_invariants(case, dk, dv, "cfg4")
 
+    c64 = [t.to(device=device, dtype=torch.float64) for t in (case.q, case.k, case.v, case.dout)]
+    meta = case.oracle_args()
+    o_r, lse_r, dq_r, dk_r, dv_r = chunked_forward_backward(*c64, False, *meta, chunk=2048)
+    torch.cuda.synchronize()
+    print(f"[cfg4 full] outlier channel {case.meta['outlier_channel']} x{case.meta['outlier_scale']} on q, k", flush=True)
+    errs = {
+        "o": report("O", out, o_r, 2e-2),
+        "lse": report("lse", lse, lse_r, 1e-2, channel_dim=False),
+        "dq": report("dQ", dq, dq_r, 5e-2),
+        "dk": report("dK", dk, dk_r, 5e-2),
+        "dv": report("dV", dv, dv_r, 5e-2),
+    }
+    assert errs["o"] <= 2e-2 and errs["lse"] <= 1e-2, errs
+    for name, got, ref in (("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
+        assert_channel_bound(name, got, ref)
+
+    # The GPU fp64 evaluation of the oracle agrees with the CPU oracle on sampled rows.
     n, p = case.seq_lens[0], case.prefixes[0]
     hq, hkv, d = case.q.shape[1], case.k.shape[1], case.q.shape[2]
     G = hq // hkv
     scale = 1.0 / math.sqrt(d)
     gen = torch.Generator().manual_seed(4)
-    rows = torch.cat([torch.tensor([0, p - 1, p, n - 1]), torch.randint(0, n, (28,), generator=gen)]).unique()
-    qf = case.q.float()[rows]                           # [R, Hq, D]
-    kf = case.k.float().repeat_interleave(G, dim=1)     # [n, Hq, D]
-    vf = case.v.float().repeat_interleave(G, dim=1)
-    dof = case.dout.float()[rows]
-    worst = {"o": 0.0, "lse": 0.0, "dq": 0.0}
-    for h in range(hq):
-        s = (qf[:, h] @ kf[:, h].T) * scale                              # [R, n]
-        allowed = torch.arange(n)[None, :] < torch.clamp(rows[:, None] + 1, min=p)
-        s = s.masked_fill(~allowed, float("-inf"))
-        ref_lse = torch.logsumexp(s, dim=1)
-        pr = torch.exp(s - ref_lse[:, None])
-        o = pr @ vf[:, h]
-        dp = dof[:, h] @ vf[:, h].T
-        o_stored = out[rows, h].float().cpu()
-        dq_fp32 = (pr * (dp - (dof[:, h] * o).sum(1, keepdim=True)) * scale) @ kf[:, h]
-        pr_saved = torch.exp(s - lse[h, rows].cpu()[:, None])
-        ds = pr_saved * (dp - (dof[:, h] * o_stored).sum(1, keepdim=True))
-        dq_bf16o = (ds.bfloat16().float() @ kf[:, h]) * scale
-        ds_ref = pr * (dp - (dof[:, h] * o.bfloat16().float()).sum(1, keepdim=True))
-        dq_ref_o = (ds_ref.bfloat16().float() @ kf[:, h]) * scale
-        got = dq[rows, h].float().cpu()
-        worst["o"] = max(worst["o"], (o_stored - o).abs().max().item())
-        worst["lse"] = max(worst["lse"], (lse[h, rows].cpu() - ref_lse).abs().max().item())
-        worst["dq"] = max(worst["dq"], (got - dq_bf16o).abs().max().item())
-        worst["dq_vs_fp32"] = max(worst.get("dq_vs_fp32", 0.0), (got - dq_fp32).abs().max().item())
-        worst["intrinsic"] = max(worst.get("intrinsic", 0.0), (dq_ref_o - dq_fp32).abs().max().item())
-    print(f"[cfg4 sampled rows] {worst} rows={rows.numel()}", flush=True)
-    assert worst["o"] <= 2e-2 and worst["lse"] <= 1e-2 and worst["dq"] <= 5e-2, worst
-    assert worst["dq_vs_fp32"] <= 1.5 * worst["intrinsic"] + 5e-2, worst
-    # the sampled mask agrees with the reference mask statement
-    assert torch.equal(prefixlm_mask(n, p, False)[rows[:4]], (torch.arange(n)[None, :] <
-                                                             torch.clamp(rows[:4, None] + 1, min=p)))
+    rows = torch.cat([torch.tensor([0, p - 1, p, n - 1]), torch.randint(0, n, (12,), generator=gen)]).unique()
+    qf, kf, vf = case.q.double()[rows], case.k.double(), case.v.double()
+    dof = case.dout.double()[rows]
+    allowed = torch.arange(n)[None, :] < torch.clamp(rows[:, None] + 1, min=p)
+    assert torch.equal(prefixlm_mask(n, p, False)[rows[:4]], allowed[:4])
+    for h in range(0, hq, 7):
+        kh, vh = kf[:, h // G], vf[:, h // G]
+        s = ((qf[:, h] @ kh.T) * scale).masked_fill(~allowed, float("-inf"))
+        l_ = torch.logsumexp(s, dim=1)
+        pr = torch.exp(s - l_[:, None])
+        o = pr @ vh
+        ds = pr * (dof[:, h] @ vh.T - (dof[:, h] * o).sum(1, keepdim=True)) * scale
+        torch.testing.assert_close(o_r[rows, h].cpu(), o, rtol=1e-9, atol=1e-9)
+        torch.testing.assert_close(lse_r[h, rows].cpu(), l_, rtol=1e-9, atol=1e-9)
+        torch.testing.assert_close(dq_r[rows, h].cpu(), ds @ kh, rtol=1e-9, atol=1e-9)
+
+
+def test_split_decision_on_the_device(device):
+    """AUTO splits P and dS exactly when softmax_scale * max|K| > 0.75: bitwise ALWAYS on an
+    outlier input and bitwise NEVER on a plain one (so the decision is what changes the
+    result), and on the outlier input the split brings dQ within the bar of the fp64 closed
+    form (5e-2, or two bf16 half-ulps of a channel's max|ref| above it), which the unsplit
+    kernels miss."""
+    mode = P._split_mode
+    try:
+        for outlier, same in ((20.0, "always"), (None, "never")):
+            case = make_case([1500, 700], [600, 0], 8, 2, 128, seed=31, dtype=torch.bfloat16, outlier=outlier)
+            res = {}
+            for m in ("auto", "always", "never"):
+                P.set_split_mode(m)
+                res[m] = run(case, device)
+            for a, b in zip(res["auto"], res[same]):
+                assert torch.equal(a, b), (outlier, same)
+            if outlier is not None:
+                c64 = [t.to(device=device, dtype=torch.float64) for t in (case.q, case.k, case.v, case.dout)]
+                ref = chunked_forward_backward(*c64, False, *case.oracle_args())
+                for i, name in ((0, "O"), (2, "dQ"), (3, "dK"), (4, "dV")):
+                    r_split = channel_excess(res["always"][i], ref[i]).max().item()
+                    r_plain = channel_excess(res["never"][i], ref[i]).max().item()
+                    print(f"[split] outlier {name}: error / bound split {r_split:.3g}, unsplit {r_plain:.3g}",
+                          flush=True)
+                    assert r_split <= 1, (name, r_split)
+                assert channel_excess(res["never"][2], ref[2]).max().item() > 1  # dQ needs the split
+    finally:
+        P._split_mode = mode

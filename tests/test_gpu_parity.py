@@ -294,3 +294,82 @@ def test_graph_replay_matches_eager(device, d):
         torch.cuda.synchronize()
         for got, ref in zip((out, lse, dq, dk, dv), eager):
             assert torch.equal(got, ref)
+
+
+def _cut(case, total):
+    """The same batch with total_seqlen ending before the last sequence's end."""
+    case.total_seqlen = torch.tensor(int(total), dtype=torch.int64)
+    return case
+
+
+CUTS = [
+    # seq_lens, prefixes, hq, hkv, d, total: where total_seqlen ends
+    ([300, 500], [50, 100], 8, 2, 128, 300 + 250),   # inside the second sequence, past its prefix
+    ([300, 500], [50, 400], 8, 2, 128, 300 + 250),   # inside the second sequence's prefix
+    ([700], [64], 4, 1, 128, 333),                   # mid-tile, past the prefix
+    ([300, 500], [50, 100], 8, 2, 64, 300 + 250),    # head_dim 64 kernels
+]
+
+
+@pytest.mark.parametrize("handoff", [True, False], ids=["handoff", "recompute"])
+@pytest.mark.parametrize("idx", range(len(CUTS)))
+def test_total_seqlen_inside_a_sequence(device, idx, handoff, dscore_limit):
+    """total_seqlen ending inside a sequence: rows from total on are outputs of zero (O, dQ)
+    and carry no gradient, while keys there remain keys of the earlier rows that see them
+    (dense.py:79-80).  Keys past the last active query in the causal part get dK = dV = 0."""
+    dscore_limit((4 << 30) if handoff else 0)
+    seq_lens, prefixes, hq, hkv, d, total = CUTS[idx]
+    case = _cut(make_case(seq_lens, prefixes, hq, hkv, d, seed=40 + idx, dtype=torch.bfloat16), total)
+    check(case, device, label=f"cut{idx} total={total} handoff={handoff}")
+
+
+def test_understated_max_seqlen_all(device):
+    """max_seqlen_all smaller than a sequence: the validated call raises ValueError; without
+    validation the result is still correct (the tile lists do not depend on it, and dQ falls
+    back from the score-gradient region, which it sizes, to the recompute)."""
+    from mimir_amd import prefixlm as P
+
+    case = make_case([900, 300], [400, 0], 8, 2, 128, seed=50, dtype=torch.bfloat16)
+    case.max_seqlen_all = torch.tensor(300, dtype=torch.int64)
+    saved = P._validate_metadata
+    try:
+        P.set_validate_metadata(True)
+        with pytest.raises(ValueError, match="max_seqlen_all"):
+            run_gpu(case, device)
+        P.set_validate_metadata(False)
+        check(case, device, label="max_seqlen_all understated")
+    finally:
+        P._validate_metadata = saved
+
+
+def test_workspace_oom_falls_back_to_recompute(device, monkeypatch):
+    """If the backward workspace with the score-gradient region cannot be allocated, the
+    backward runs with the small workspace and the recomputing dQ: same dK / dV bit for
+    bit, dQ within the bar."""
+    from mimir_amd import prefixlm as P
+
+    from mimir_amd import _capi
+
+    case = make_case([900, 333], [450, 0], 8, 2, 128, seed=51, dtype=torch.bfloat16)
+    base = run_gpu(case, device)
+    # the workspace without the region: anything larger is the hand-off request
+    small = _capi.load().mimir_prefixlm_bwd_workspace_bytes(case.T, 8, 2, 900)
+    real_empty = torch.empty
+    refused = []
+
+    def empty(*shape, **kw):
+        n = 1
+        for s in (shape[0] if len(shape) == 1 and isinstance(shape[0], (tuple, list)) else shape):
+            n *= int(s)
+        if kw.get("dtype") is torch.float32 and n * 4 > small and not refused:
+            refused.append(n)
+            raise torch.cuda.OutOfMemoryError("refused by the test")
+        return real_empty(*shape, **kw)
+
+    monkeypatch.setattr(P.torch, "empty", empty)
+    got = run_gpu(case, device)
+    monkeypatch.undo()
+    assert refused, "the hand-off workspace was never requested"
+    assert torch.equal(got["dk"], base["dk"]) and torch.equal(got["dv"], base["dv"])
+    assert (got["dq"] - base["dq"]).abs().max().item() <= 1e-2
+    check(case, device, label="after OOM fallback")

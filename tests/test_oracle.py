@@ -199,3 +199,56 @@ def test_padding_rows_get_no_query_gradient():
                                 False, *c.oracle_args())
     assert torch.count_nonzero(dq[10:]) == 0
     assert torch.count_nonzero(dk[10:]) == 0 and torch.count_nonzero(dv[10:]) == 0
+
+
+# ---------------------------------------------------------------- chunked closed form
+def _with_total(case, total):
+    case.total_seqlen = torch.tensor(int(total), dtype=torch.int64)
+    return case
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 7, 64])
+@pytest.mark.parametrize("shape", [
+    # seq_lens, prefixes, hq, hkv, pad_to, is_causal, total (None: all tokens)
+    ([9, 1, 12], [4, 1, 0], 4, 2, 25, False, None),
+    ([9, 1, 12], [4, 1, 0], 4, 4, None, True, None),
+    ([16, 7], [16, 3], 6, 2, None, False, 20),     # total ends inside the second sequence, past its prefix
+    ([16, 7], [5, 3], 2, 1, None, False, 3),       # total ends inside the first sequence's prefix
+])
+def test_chunked_forward_backward_equals_dense(chunk, shape):
+    """The chunked restatement equals the per-sequence dense forward, the closed-form lse and
+    the closed-form backward (all fp64), for every chunk size: a dropped mask term, a wrong
+    chunk boundary, a missing GQA sum or a wrong delta would show."""
+    from oracle.prefixlm_oracle import chunked_forward_backward
+
+    seq_lens, prefixes, hq, hkv, pad_to, causal, total = shape
+    c = _case(seq_lens, prefixes, hq=hq, hkv=hkv, d=8, seed=7, pad_to=pad_to, is_causal=causal)
+    if total is not None:
+        _with_total(c, total)
+    args = c.oracle_args()
+    o_ref = dense_forward(c.q, c.k, c.v, causal, *args)
+    lse_ref = dense_lse(c.q, c.k, causal, *args)
+    dq_ref, dk_ref, dv_ref = dense_backward(c.q, c.k, c.v, o_ref, c.dout, causal, *args)
+    o, lse, dq, dk, dv = chunked_forward_backward(c.q, c.k, c.v, c.dout, causal, *args, chunk=chunk)
+    for got, ref in ((o, o_ref), (dq, dq_ref), (dk, dk_ref), (dv, dv_ref)):
+        torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
+    fin = torch.isfinite(lse_ref)
+    assert torch.equal(fin, torch.isfinite(lse))
+    torch.testing.assert_close(lse[fin], lse_ref[fin], rtol=1e-12, atol=1e-12)
+
+
+def test_backward_with_total_inside_a_sequence_matches_autograd():
+    """total_seqlen ending inside a sequence past its prefix: O rows from total on are zero
+    (dense.py:79-80), so no gradient flows from them, while the keys there stay keys for
+    earlier prefix rows.  The closed form agrees with autograd through dense_forward."""
+    c = _with_total(_case([12, 9], [8, 2], hq=4, hkv=2, d=8, seed=3), 16)
+    args = c.oracle_args()
+    q, k, v = (t.clone().requires_grad_(True) for t in (c.q, c.k, c.v))
+    dense_forward_autograd(q, k, v, False, *args).backward(c.dout)
+    o = dense_forward(c.q, c.k, c.v, False, *args)
+    dq, dk, dv = dense_backward(c.q, c.k, c.v, o, c.dout, False, *args)
+    for got, ref in ((dq, q.grad), (dk, k.grad), (dv, v.grad)):
+        torch.testing.assert_close(got, ref, rtol=1e-10, atol=1e-10)
+    # keys of the second sequence past total still receive gradient from its prefix rows
+    assert dk[12 + 4:12 + 8].abs().sum() == 0  # keys 4..7 of seq 2 are in its causal part: rows >= 4 only
+    assert dq[16:].abs().sum() == 0
