@@ -207,6 +207,18 @@ size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs,
  * src/mimir/model/flash_attention_prefixlm_dense.py:19-81. */
 int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* params, void* stream);
 
+/* The forward for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  It ignores params->workspace and keeps its
+ * work list and K-scan slots in a fixed device array of 128 KiB inside the
+ * library (one per GPU, held until the process ends): a call whose
+ * mimir_prefixlm_fwd_workspace_bytes exceeds 128 KiB fails with
+ * MIMIR_ERR_UNSUPPORTED_SHAPE before any device work (it fits while
+ * ceil(total_tokens / 128) + numseqs <= 16128).  It calls no hipMalloc / hipFree.  Every call on one GPU
+ * shares that array, so calls that overlap on one GPU (two streams or threads)
+ * race; the array needs no clearing between calls.  Outputs as mimir_prefixlm_fwd. */
+int mimir_prefixlm_fwd_noalloc(const MimirPrefixLMFwdParams* params, void* stream);
+
 /* Backward: dq, dk, dv from dout, out and lse.  Deterministic and atomic-free.
  * Replaces the FA3 backward custom op src/mimir/model/flash_attention_prefixlm_v2.py:165-227,
  * FA4's backward reached through fa4.py:153-179,309-331, and the Metal split

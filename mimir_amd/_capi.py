@@ -117,6 +117,7 @@ BWD_STAGE_ALL = 15
 
 EXPORTED_SYMBOLS = (
     "mimir_prefixlm_fwd",
+    "mimir_prefixlm_fwd_noalloc",
     "mimir_prefixlm_bwd",
     "mimir_prefixlm_bwd_stages",
     "mimir_prefixlm_fwd_workspace_bytes",
@@ -155,6 +156,8 @@ def load() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(LIB_PATH))
         lib.mimir_prefixlm_fwd.argtypes = [ctypes.POINTER(FwdParams), _vp]
         lib.mimir_prefixlm_fwd.restype = ctypes.c_int
+        lib.mimir_prefixlm_fwd_noalloc.argtypes = [ctypes.POINTER(FwdParams), _vp]
+        lib.mimir_prefixlm_fwd_noalloc.restype = ctypes.c_int
         lib.mimir_prefixlm_bwd.argtypes = [ctypes.POINTER(BwdParams), _vp]
         lib.mimir_prefixlm_bwd.restype = ctypes.c_int
         lib.mimir_prefixlm_bwd_stages.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int, _vp]

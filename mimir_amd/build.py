@@ -49,6 +49,7 @@ SOURCES = [
     "prefixlm_prologue.hip",
     "prefixlm_layer.hip",
     "prefixlm_cache_bf16.hip",
+    "prefixlm_noalloc.hip",
 ]
 
 
