@@ -16,9 +16,9 @@ when dQ recomputes S and dP, that is not counted), so the three add up to the
 step's 14*D*Hq*N.  With the score-gradient hand-off (bf16, head_dim 128) the dQ
 kernel reads the dS blocks the dK/dV kernel stored; the line then also gives its
 streamed bytes and bandwidth (``dq_ds_bytes``, ``dq_ds_gbs``).
-Kernel durations come from a second pass of K steps with the stages serialized
+Kernel durations come from a separate pass of K steps with the stages serialized
 (``mimir_prefixlm_bwd_stages``) and HIP events recorded on the launch stream
-between them.  The CPU baseline times the oracle's restatement of the reference
+between them; that pass and the per-step medians run before the timed region.  The CPU baseline times the oracle's restatement of the reference
 masked-SDPA path (fp32, autograd) on a bounded sample of the same batch.
 
 Prints exactly one JSON line.
@@ -501,21 +501,10 @@ def main() -> int:
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(K)]
     for _ in range(args.warmup):
         step()
-    staged_step(evs[0])
     torch.cuda.synchronize()
 
-    # Timed region: K whole steps.
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_start.record()
-    for _ in range(K):
-        step()
-    t_end.record()
-    torch.cuda.synchronize()
-    total_ms = t_start.elapsed_time(t_end)
-    ms_per_step = total_ms / K
-
+    # The measurement passes run first and the timed region last, so that the
+    # timed steps find the GPU clocks settled.
     # Forward and forward + backward per step, HIP events on the launch stream: medians of K runs.
     pe = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
     for k in range(K):
@@ -533,6 +522,19 @@ def main() -> int:
     for k in range(K):
         staged_step(evs[k])
     torch.cuda.synchronize()
+
+    # Timed region: K whole steps.
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for _ in range(K):
+        step()
+    t_end.record()
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    ms_per_step = total_ms / K
+
     stage_ms = {name: [evs[k][i].elapsed_time(evs[k][i + 1]) for k in range(K)] for i, (name, _) in enumerate(stages)}
     stage_avg = {name: sum(v) / len(v) for name, v in stage_ms.items()}
     stage_med = {name: statistics.median(v) for name, v in stage_ms.items()}
