@@ -198,8 +198,11 @@ def copy_calibration(torch, dev, mib: int, reps: int) -> int:
 def layer_bench(torch, dev, args) -> int:
     """The attention layer core of src/mimir/model/layers.py:182-239 on a workload's shapes.
 
-    fused:   mimir_amd.layer.gated_attention (RoPE kernel on q / k, gate in the
-             attention store and its backward in the delta rows, one gqkv gradient)
+    fused:   mimir_amd.layer.gated_attention (bf16: q rotated inside the attention
+             forward, which also writes the rotated copy the backward streams, k by
+             one RoPE kernel pass, dQ / dK mapped back in the backward's stores; the
+             gate in the attention store and its backward in the delta rows; one gqkv
+             gradient)
     unfused: the reference's composition -- split views, fp32 torch RoPE
              (layers.py:24-40), the same prefix-LM operator, torch.sigmoid(gate) * attn
     Both run forward + backward from the gqkv projection output to the o_proj input.

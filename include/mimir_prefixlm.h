@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MIMIR_PREFIXLM_ABI_VERSION 5
+#define MIMIR_PREFIXLM_ABI_VERSION 6
 
 /* Element types of q/k/v/out/dout/dq/dk/dv (lse and the workspace are float32). */
 enum MimirDType {
@@ -109,6 +109,19 @@ typedef struct MimirPrefixLMFwdParams {
    * (MimirPrefixLMBwdParams.split_flag), the backward follows the same decision
    * without scanning K again and reads out_lo only when it is set. */
   int32_t* split_flag;        /* device int32 [1] */
+  /* Optional rotary position embedding of q inside the kernel (bf16 only;
+   * rope_cos NULL: none), replacing the apply_rotary_pos_emb of q before the
+   * attention call (src/mimir/model/layers.py:186-189, rotate-half convention
+   * layers.py:24-40): q is then the unrotated query, rotated where the kernel
+   * loads it, with the roundings of mimir_prefixlm_rope; k must already be the
+   * rotated key (mimir_prefixlm_rope: the kernel streams K through LDS).  With
+   * q_rope non-NULL the kernel also writes the rotated q there (the rows below
+   * total_seqlen of every sequence), the q operand of the backward. */
+  const float* rope_cos;      /* [T, D] float32, 16-byte aligned rows */
+  const float* rope_sin;      /* [T, D] float32 */
+  int64_t rope_stride_token;  /* elements between rows of rope_cos / rope_sin (multiple of 4) */
+  void* q_rope;               /* optional out [T, Hq, D] */
+  int64_t q_rope_stride_token, q_rope_stride_head;
 } MimirPrefixLMFwdParams;
 
 /* Whether the bf16 kernels carry the softmax probabilities P and the score
@@ -191,6 +204,15 @@ typedef struct MimirPrefixLMBwdParams {
   int64_t out_lo_stride_token, out_lo_stride_head;
   int32_t split_mode;         /* enum MimirSplitMode (bf16; dS in dK = dS^T Q and dQ = dS K) */
   const int32_t* split_flag;  /* the forward's recorded decision (device int32 [1]) or NULL */
+  /* Optional gradient of a rotary position embedding inside the kernels (bf16
+   * only; rope_cos NULL: none): q and k are the rotated operands the forward
+   * used, and dq / dk receive the gradients of the unrotated q / k -- the bf16
+   * gradient of the rotated operand mapped back in the kernels' stores exactly
+   * as mimir_prefixlm_rope with inverse = 1 maps it (what autograd does for
+   * layers.py:186-189).  Same tables as MimirPrefixLMFwdParams.rope_cos. */
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_stride_token;
 } MimirPrefixLMBwdParams;
 
 /* Bytes of device workspace the forward needs: the heaviest-first tile work list

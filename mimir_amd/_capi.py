@@ -16,7 +16,7 @@ from pathlib import Path
 
 # MIMIR_PREFIXLM_LIB overrides the in-tree library (e.g. to A/B two builds).
 LIB_PATH = Path(os.environ.get("MIMIR_PREFIXLM_LIB") or Path(__file__).resolve().parent / "_lib" / "libmimir_prefixlm.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_FLOAT32 = 0
 DTYPE_BFLOAT16 = 1
@@ -53,6 +53,8 @@ class FwdParams(ctypes.Structure):
         ("gated_out", _vp), ("gated_out_stride_token", _i64), ("gated_out_stride_head", _i64),
         ("out_lo", _vp), ("out_lo_stride_token", _i64), ("out_lo_stride_head", _i64),
         ("split_mode", _i32), ("split_flag", _vp),
+        ("rope_cos", _vp), ("rope_sin", _vp), ("rope_stride_token", _i64),
+        ("q_rope", _vp), ("q_rope_stride_token", _i64), ("q_rope_stride_head", _i64),
     ]
 
 
@@ -79,6 +81,7 @@ class BwdParams(ctypes.Structure):
         ("dscore_limit_bytes", ctypes.c_size_t),
         ("out_lo", _vp), ("out_lo_stride_token", _i64), ("out_lo_stride_head", _i64),
         ("split_mode", _i32), ("split_flag", _vp),
+        ("rope_cos", _vp), ("rope_sin", _vp), ("rope_stride_token", _i64),
     ]
 
 

@@ -46,6 +46,7 @@ struct BwdArgs {
   const int* split_flag;  // the forward's recorded split decision, or NULL
   int split_mode;    // MimirSplitMode
   int dq_companion;  // 1: the recomputing dQ kernel enqueued beside the hand-off's
+  RopeTab rope;      // optional: dQ / dK stored as gradients of the unrotated q / k
 };
 
 // queue[kDsIncomplete]: set by the dK / dV kernel when a score-gradient tile fell

@@ -270,15 +270,13 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
-      f32x4 tk, tv;
+      f32x4 tv;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        tk[e] = dkacc[dt][4 * rg + e] * a.scale;
-        tv[e] = dvacc[dt][4 * rg + e];
-      }
-      *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tk, bf16x4);
+      for (int e = 0; e < 4; ++e) tv[e] = dvacc[dt][4 * rg + e];
       *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
     }
+  grad_out<DT>(dkacc, a.scale, rope_args(a.rope), g.start + kpos, hi,
+               [&](int dt, int rg, bf16x4 v) { *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = v; });
 }
 
 

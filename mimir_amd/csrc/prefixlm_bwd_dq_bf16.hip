@@ -193,15 +193,9 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   constexpr int kRowsPerInst = 64 / kUnits;
   static_assert(32 * kPitch <= L::kElems, "a wave's rows fit its stage object");
   bf16_t* const stage = wave == 0 ? sK0 : wave == 1 ? sV0 : wave == 2 ? sK1 : sV1;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      f32x4 t;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) t[e] = dqacc[dt][4 * rg + e] * a.scale;
-      *(bf16x4*)&stage[l32 * kPitch + 32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
-    }
+  grad_out<DT>(dqacc, a.scale, a.rope, min(g.start + qa + l32, a.T - 1), hi, [&](int dt, int rg, bf16x4 v) {
+    *(bf16x4*)&stage[l32 * kPitch + 32 * dt + 8 * rg + 4 * hi] = v;
+  });
   // The LDS unit runs one wave's accesses in order: the reads below see the writes above.
   __asm__ volatile("" ::: "memory");
   const int u = lane % kUnits;

@@ -167,15 +167,9 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
   static_assert(2 * 32 * kPitch <= L::kElems, "two waves' rows fit one K stage object");
   bf16_t* const stage = (wave < 2 ? sK0 : sK1) + (wave & 1) * 32 * kPitch;
   const int srow = ds_query_of(l32);
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      f32x4 t;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) t[e] = dqacc[dt][4 * rg + e] * a.scale;
-      *(bf16x4*)&stage[srow * kPitch + 32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(t, bf16x4);
-    }
+  grad_out<DT>(dqacc, a.scale, a.rope, min(g.start + qa + srow, a.T - 1), hi, [&](int dt, int rg, bf16x4 v) {
+    *(bf16x4*)&stage[srow * kPitch + 32 * dt + 8 * rg + 4 * hi] = v;
+  });
   // The LDS unit runs one wave's accesses in order: the reads below see the writes above.
   __asm__ volatile("" ::: "memory");
   const int u = lane % kUnits;

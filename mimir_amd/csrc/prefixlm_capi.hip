@@ -108,6 +108,19 @@ int check_operand(const char* name, const void* ptr, int64_t st, int64_t sh, int
   return MIMIR_OK;
 }
 
+// RoPE tables of the fused rotation (bf16 kernels only).
+int check_rope(int dtype, int D, const float* cos, const float* sin, int64_t st) {
+  if (cos == nullptr && sin == nullptr) return MIMIR_OK;
+  if (dtype != MIMIR_DTYPE_BFLOAT16)
+    return fail(MIMIR_ERR_UNSUPPORTED_DTYPE, "RoPE inside the attention kernels is bfloat16 only; for float32 "
+                                             "rotate with mimir_prefixlm_rope");
+  if (cos == nullptr || sin == nullptr) return fail(MIMIR_ERR_INVALID_ARGUMENT, "rope_cos and rope_sin go together");
+  if (!aligned16(cos) || !aligned16(sin) || st % 4 != 0 || st < D)
+    return fail(MIMIR_ERR_INVALID_ARGUMENT, "rope_cos / rope_sin rows must be 16-byte aligned float32 rows of at "
+                                            "least head_dim elements (rope_stride_token a multiple of 4)");
+  return MIMIR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -193,6 +206,12 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* p, void* stream_) {
   if (p->split_mode < MIMIR_SPLIT_AUTO || p->split_mode > MIMIR_SPLIT_NEVER)
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "split_mode must be MIMIR_SPLIT_AUTO, _ALWAYS or _NEVER");
   if (((uintptr_t)p->split_flag & 3u) != 0) return fail(MIMIR_ERR_INVALID_ARGUMENT, "split_flag must be 4-byte aligned");
+  if ((rc = check_rope(dt, D, p->rope_cos, p->rope_sin, p->rope_stride_token))) return rc;
+  if (p->q_rope != nullptr) {
+    if (p->rope_cos == nullptr) return fail(MIMIR_ERR_INVALID_ARGUMENT, "q_rope needs rope_cos / rope_sin");
+    if ((rc = check_operand("q_rope", p->q_rope, p->q_rope_stride_token, p->q_rope_stride_head, D, dt, rows)))
+      return rc;
+  }
   if (p->out_lo != nullptr) {
     if (dt != MIMIR_DTYPE_BFLOAT16)
       return fail(MIMIR_ERR_INVALID_ARGUMENT, "out_lo is a bfloat16 output (float32 needs no low half)");
@@ -264,6 +283,7 @@ int mimir_prefixlm_bwd_stages(const MimirPrefixLMBwdParams* p, int stages, void*
   if (p->split_mode < MIMIR_SPLIT_AUTO || p->split_mode > MIMIR_SPLIT_NEVER)
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "split_mode must be MIMIR_SPLIT_AUTO, _ALWAYS or _NEVER");
   if (((uintptr_t)p->split_flag & 3u) != 0) return fail(MIMIR_ERR_INVALID_ARGUMENT, "split_flag must be 4-byte aligned");
+  if ((rc = check_rope(dt, D, p->rope_cos, p->rope_sin, p->rope_stride_token))) return rc;
   const size_t need = mimir_prefixlm_bwd_workspace_size(p);
   if (p->workspace == nullptr || p->workspace_bytes < need || !aligned16(p->workspace))
     return fail(MIMIR_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned and hold at least " +

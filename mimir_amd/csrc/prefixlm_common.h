@@ -171,6 +171,112 @@ __device__ __forceinline__ float sigmoid_bf16(float x) {
 }
 
 // ---------------------------------------------------------------------------
+// Rotary position embedding inside the attention kernels (rotate-half
+// convention, src/mimir/model/layers.py:24-40): float32 cos / sin rows [T, D],
+// one per token; column d pairs with d + D/2.  A register-resident operand is
+// rotated where it is loaded (Q in the forward), and the gradients of the
+// rotated operands are mapped back to the unrotated ones where they are stored
+// (dQ, dK), with the roundings of prefixlm_layer.hip's rope_kernel:
+//   y1  = round(x1 * cos[d] - x2 * sin[d])
+//   y2  = round(x2 * cos[d + D/2] + x1 * sin[d + D/2])
+//   dx1 = round(round(g1 * cos[d]) + round(g2 * sin[d + D/2]))
+//   dx2 = round(round(g2 * cos[d + D/2]) - round(g1 * sin[d]))
+// (fp32 products and sums, no contraction; round = to bf16; g the bf16 gradient
+// of the rotated operand).
+// ---------------------------------------------------------------------------
+struct RopeTab {
+  const float* cos;  // nullptr: no RoPE
+  const float* sin;
+  int64_t st;        // elements between the rows of cos / sin
+};
+
+// The tables re-read from the kernel arguments where they are used (a volatile
+// read cannot be hoisted), so that they hold no scalar registers across a tile loop.
+__device__ __forceinline__ RopeTab rope_args(const RopeTab& r) {
+  const volatile RopeTab* p = &r;
+  return RopeTab{p->cos, p->sin, p->st};
+}
+
+// Rotation of four column pairs (d1 + e, d1 + e + half), e < 4, of token t.
+__device__ __forceinline__ void rope_rotate4(const RopeTab& r, int64_t t, int d1, int half, f32x4 x1, f32x4 x2,
+                                             bf16x4& y1, bf16x4& y2) {
+#pragma clang fp contract(off)
+  const float* cr = r.cos + t * r.st;
+  const float* sr = r.sin + t * r.st;
+  const f32x4 c1 = *(const f32x4*)(cr + d1), c2 = *(const f32x4*)(cr + d1 + half);
+  const f32x4 s1 = *(const f32x4*)(sr + d1), s2 = *(const f32x4*)(sr + d1 + half);
+  f32x4 a, b;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = x1[e] * c1[e] - x2[e] * s1[e];
+    b[e] = x2[e] * c2[e] + x1[e] * s2[e];
+  }
+  y1 = __builtin_convertvector(a, bf16x4);
+  y2 = __builtin_convertvector(b, bf16x4);
+}
+
+// Gradient of the rotation for four column pairs: g1, g2 hold the bf16-rounded
+// gradients of the rotated operand (as fp32 values).
+__device__ __forceinline__ void rope_grad4(const RopeTab& r, int64_t t, int d1, int half, f32x4 g1, f32x4 g2,
+                                           bf16x4& x1, bf16x4& x2) {
+#pragma clang fp contract(off)
+  const float* cr = r.cos + t * r.st;
+  const float* sr = r.sin + t * r.st;
+  const f32x4 c1 = *(const f32x4*)(cr + d1), c2 = *(const f32x4*)(cr + d1 + half);
+  const f32x4 s1 = *(const f32x4*)(sr + d1), s2 = *(const f32x4*)(sr + d1 + half);
+  f32x4 a, b;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = round_to(g1[e] * c1[e], bf16_t()) + round_to(g2[e] * s2[e], bf16_t());
+    b[e] = round_to(g2[e] * c2[e], bf16_t()) - round_to(g1[e] * s1[e], bf16_t());
+  }
+  x1 = __builtin_convertvector(a, bf16x4);
+  x2 = __builtin_convertvector(b, bf16x4);
+}
+
+// bf16 rounding of four fp32 values, kept as fp32.
+__device__ __forceinline__ f32x4 round4(f32x4 x) {
+  return __builtin_convertvector(__builtin_convertvector(x, bf16x4), f32x4);
+}
+
+// The bf16 gradient values a lane stores for the columns 32 dt + 8 rg + 4 hi + e
+// (e < 4) of one row, from fp32 accumulators acc[dt][4 rg + e] times `scale`:
+// the rounded products, or with RoPE (rope.cos set; token t) the gradient of the
+// unrotated operand, columns of tiles dt and dt + DT / 2 paired.  put(dt, rg, v)
+// receives them.
+template <int DT, typename Put>
+__device__ __forceinline__ void grad_out(const f32x16 (&acc)[DT], float scale, const RopeTab& rope, int64_t t,
+                                         int hi, Put&& put) {
+  if (rope.cos == nullptr) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[dt][4 * rg + e] * scale;
+        put(dt, rg, __builtin_convertvector(v, bf16x4));
+      }
+  } else {
+#pragma unroll
+    for (int dt = 0; dt < DT / 2; ++dt)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        f32x4 g1, g2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          g1[e] = acc[dt][4 * rg + e] * scale;
+          g2[e] = acc[dt + DT / 2][4 * rg + e] * scale;
+        }
+        bf16x4 x1, x2;
+        rope_grad4(rope, t, 32 * dt + 8 * rg + 4 * hi, 16 * DT, round4(g1), round4(g2), x1, x2);
+        put(dt, rg, x1);
+        put(dt + DT / 2, rg, x2);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // LDS tile layout.  A [64][D] bf16 operand tile is stored with
 //   * a row stride of D/8 + 1 sixteen-byte units (one unit of padding), and
 //   * logical row k at physical row perm(k), which transposes the 4 x 4 grid

@@ -55,6 +55,9 @@ struct FwdArgs {
   const int* kscan;    // the prologue's K scan (split_mode AUTO)
   int split_mode;      // MimirSplitMode: P as bf16 hi + lo in O^T += V^T P^T
   int* split_flag;     // optional: the decision, for the backward
+  RopeTab rope;        // optional RoPE of Q, applied to the loaded fragments
+  bf16_t* q_rope;      // optional: the rotated Q rows, for the backward
+  int64_t qr_st, qr_sh;
 };
 
 // kSplit: P is not (0) / is (1) split.  The split changes the registers of the
@@ -135,6 +138,28 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   for (int ks = 0; ks < KS; ++ks) {
     const uint32_t off = (uint32_t)(((int64_t)qpos * a.q_st + 16 * ks + 8 * hi) * 2);
     qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rq, off));
+  }
+  // RoPE: fragment ks (d = 16 ks + 8 hi ..) pairs with ks + KS / 2 (d + D / 2)
+  // of the same lane.  Rows past the sequence read the last token's tables and
+  // are never stored.
+  if (a.rope.cos != nullptr) {
+    const int64_t t = min(g.start + qpos, a.T - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS / 2; ++ks) {
+      bf16x4 y1[2], y2[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f32x4 x1, x2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x1[e] = (float)qf[ks][4 * j + e];
+          x2[e] = (float)qf[ks + KS / 2][4 * j + e];
+        }
+        rope_rotate4(a.rope, t, 16 * ks + 8 * hi + 4 * j, D / 2, x1, x2, y1[j], y2[j]);
+      }
+      qf[ks] = cat8(y1[0], y1[1]);
+      qf[ks + KS / 2] = cat8(y2[0], y2[1]);
+    }
   }
   // Gated store: round(sigmoid(gate)) of this lane's output elements, formed
   // before the tile loop so that neither the gate rows' latency nor the
@@ -319,6 +344,21 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
       if constexpr (kGated != 0) *(bf16x8*)&ybase[(int64_t)r * a.y_st] = yv;
     }
   }
+  // The rotated Q rows (RoPE in the kernel) for the backward: another round
+  // through the staging rows, whole rows per store as for O.
+  if (a.q_rope != nullptr) {
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) *(bf16x8*)&stage[l32 * kPitch + 16 * ks + 8 * hi] = qf[ks];
+    __asm__ volatile("" ::: "memory");
+    bf16_t* const rbase = a.q_rope + (int64_t)(g.start + qa) * a.qr_st + (int64_t)h * a.qr_sh + u * 8;
+#pragma unroll
+    for (int j = 0; j < 32 / kRowsPerInst; ++j) {
+      const int r = j * kRowsPerInst + lane / kUnits;
+      const bf16x8 v = *(const bf16x8*)&stage[r * kPitch + u * 8];
+      if (qa + r < g.nq) *(bf16x8*)&rbase[(int64_t)r * a.qr_st] = v;
+    }
+  }
   // The low halves: with a recorded decision only when split (the backward
   // reads them only then), otherwise always.
   if (a.o_lo == nullptr || (a.split_flag != nullptr && !split)) return;
@@ -388,6 +428,9 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t str
   a.olo_st = p.out_lo_stride_token; a.olo_sh = p.out_lo_stride_head;
   a.split_mode = p.split_mode;
   a.split_flag = p.split_flag;
+  a.rope = RopeTab{p.rope_cos, p.rope_sin, p.rope_stride_token};
+  a.q_rope = (bf16_t*)p.q_rope;
+  a.qr_st = p.q_rope_stride_token; a.qr_sh = p.q_rope_stride_head;
   static_assert(kBlockM == kPlanTile, "work-list tiles are the forward's query tiles");
   const int cap = plan_capacity(p.total_tokens, p.numseqs, p.max_seqlen_all);
   int2* plan = (int2*)p.workspace;

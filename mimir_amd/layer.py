@@ -9,9 +9,12 @@ before ``o_proj``.  :func:`gated_attention` is that block, from the projection
 output to the tensor ``o_proj`` consumes:
 
 * the split is free: q / k / v / gate are strided views of gqkv, read in place;
-* RoPE runs once on q and k (``mimir_prefixlm_rope``, one pass, the reference's
-  fp32 math and rounding), and its gradient is applied in place on the dQ / dK
-  slices of the gqkv gradient;
+* RoPE (the reference's fp32 math and rounding) takes one ``mimir_prefixlm_rope``
+  pass over the adjacent q and k heads of gqkv and one inverse pass, in place,
+  over the adjacent dQ / dK heads of the gqkv gradient.  For bf16 the attention
+  kernels can do both instead (:func:`set_rope_in_kernels`): q rotated as the
+  forward loads it (the kernel also writes the rotated copy the backward
+  streams), dQ / dK mapped back in the backward's stores -- bit-identical;
 * the gate is applied in the attention kernel's store (bf16), and its backward
   is fused with the delta rows of the attention backward;
 * dQ / dK / dV and dgate are written straight into one gqkv-shaped gradient.
@@ -24,6 +27,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from typing import Optional, Tuple
 
 import torch
@@ -34,14 +38,23 @@ from . import prefixlm as P
 
 _DTYPES = {torch.float32: _capi.DTYPE_FLOAT32, torch.bfloat16: _capi.DTYPE_BFLOAT16}
 
+# Where bf16 RoPE runs: in the attention kernels ("fwd": q rotated as the forward
+# loads it; "bwd": dQ / dK mapped back in the backward's stores), or (default) in
+# one mimir_prefixlm_rope pass over the adjacent q | k heads and one inverse pass
+# over dQ | dK.  Both are bit-identical; on MI355X the separate passes measure
+# slightly faster: the kernels then read every fp32 cos / sin row once per
+# (head, tile) -- four times the bytes of the bf16 rows they rotate -- at the
+# start or end of each workgroup, which costs what the two saved passes do.
+_ROPE_IN_KERNELS = frozenset(os.environ.get("MIMIR_LAYER_ROPE_IN_KERNELS", "").replace(" ", "").split(",")) - {""}
 
-def _cos_sin_rows(t: Tensor, T: int, d: int, device, name: str) -> Tensor:
-    t = t.reshape(-1, t.shape[-1])
-    if t.shape != (T, d):
-        raise ValueError(f"{name} must hold one [head_dim] row per token: expected {(T, d)}, got {tuple(t.shape)}")
-    if t.device != device or t.dtype != torch.float32 or t.stride(-1) != 1 or t.stride(0) % 4 or t.data_ptr() % 16:
-        t = t.to(device=device, dtype=torch.float32).contiguous()
-    return t
+
+def set_rope_in_kernels(where) -> None:
+    """Where the bf16 layer applies RoPE: a subset of {"fwd", "bwd"} (empty: separate passes)."""
+    global _ROPE_IN_KERNELS
+    where = frozenset(where)
+    if not where <= {"fwd", "bwd"}:
+        raise ValueError(f"RoPE placement must be a subset of {{'fwd', 'bwd'}}, got {sorted(where)}")
+    _ROPE_IN_KERNELS = where
 
 
 def rope(x: Tensor, cos: Tensor, sin: Tensor, *, inverse: bool = False, out: Optional[Tensor] = None) -> Tensor:
@@ -58,8 +71,8 @@ def rope(x: Tensor, cos: Tensor, sin: Tensor, *, inverse: bool = False, out: Opt
     if x.dtype not in _DTYPES:
         raise TypeError(f"RoPE supports float32 and bfloat16 tensors only, got {x.dtype}")
     T, H, d = x.shape
-    cos = _cos_sin_rows(cos, T, d, x.device, "cos")
-    sin = _cos_sin_rows(sin, T, d, x.device, "sin")
+    cos = P.rope_rows(cos, T, d, x.device, "cos")
+    sin = P.rope_rows(sin, T, d, x.device, "sin")
     if cos.stride(0) != sin.stride(0):
         sin = sin.contiguous()
         cos = cos.contiguous()
@@ -101,18 +114,26 @@ class _GatedAttention(torch.autograd.Function):
                 numseqs, max_seqlen_all, softmax_scale):
         lib = _capi.load()
         T, d, g3, gate, q, k, v = _split(gqkv, hq, hkv)
+        bf16 = gqkv.dtype == torch.bfloat16
+        fused = bf16 and cos is not None and "fwd" in _ROPE_IN_KERNELS  # q rotated inside the attention kernel
+        q_in = q
         if cos is not None:
-            q = rope(q, cos, sin)
-            k = rope(k, cos, sin)
+            if fused:
+                q = torch.empty((T, hq, d), dtype=q.dtype, device=q.device)  # the kernel's rotated copy
+                k = rope(k, cos, sin)
+            else:
+                # q and k are adjacent head ranges of gqkv: one pass rotates both
+                qk = rope(g3[:, hq:2 * hq + hkv], cos, sin)
+                q, k = qk[:, :hq], qk[:, hq:]
         y = torch.empty((T, hq, d), dtype=gqkv.dtype, device=gqkv.device)
         # bf16: the split decision and, when the kernels split, the low half of the
         # attention output (for the backward's delta row sums)
-        lo = gqkv.dtype == torch.bfloat16
-        out_lo = torch.empty_like(y) if lo else y.new_empty(0)
-        flag = torch.empty(1 if lo else 0, dtype=torch.int32, device=y.device)
-        p, out, lse, keep = P.prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
-                                          numseqs, max_seqlen_all, softmax_scale, gate=gate, gated_out=y,
-                                          out_lo=out_lo if lo else None, split_flag=flag)
+        out_lo = torch.empty_like(y) if bf16 else y.new_empty(0)
+        flag = torch.empty(1 if bf16 else 0, dtype=torch.int32, device=y.device)
+        p, out, lse, keep = P.prepare_fwd(q_in if fused else q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
+                                          total_seqlen, numseqs, max_seqlen_all, softmax_scale, gate=gate,
+                                          gated_out=y, out_lo=out_lo if bf16 else None, split_flag=flag,
+                                          rope=(cos, sin) if fused else None, q_rope=q if fused else None)
         _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), P._stream(y.device)))
         ctx.save_for_backward(gqkv, q, k, out, lse, out_lo, flag, cos, sin, prefix_lens, causal_lens, cu_seqlens)
         ctx.meta = (hq, hkv, is_causal, total_seqlen, numseqs, max_seqlen_all, softmax_scale)
@@ -127,13 +148,15 @@ class _GatedAttention(torch.autograd.Function):
         dg3 = torch.empty_like(g3)
         dgate, dq, dk, dv = dg3[:, :hq], dg3[:, hq:2 * hq], dg3[:, 2 * hq:2 * hq + hkv], dg3[:, 2 * hq + hkv:]
         dy3 = dy.reshape(T, hq, d)
+        fused = gqkv.dtype == torch.bfloat16 and cos is not None and "bwd" in _ROPE_IN_KERNELS
         p, dq, dk, dv, keep = P.prepare_bwd(dy3, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens,
                                             total_seqlen, numseqs, max_seqlen_all, softmax_scale, gate=gate,
-                                            dgate=dgate, dq=dq, dk=dk, dv=dv, out_lo=out_lo, split_flag=flag)
+                                            dgate=dgate, dq=dq, dk=dk, dv=dv, out_lo=out_lo, split_flag=flag,
+                                            rope=(cos, sin) if fused else None)
         _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd(ctypes.byref(p), P._stream(dg3.device)))
-        if cos is not None:
-            rope(dq, cos, sin, inverse=True, out=dq)
-            rope(dk, cos, sin, inverse=True, out=dk)
+        if cos is not None and not fused:
+            dqk = dg3[:, hq:2 * hq + hkv]  # dQ and dK, adjacent: one pass maps both back
+            rope(dqk, cos, sin, inverse=True, out=dqk)
         return (dg3.reshape(gqkv.shape),) + (None,) * 12
 
 

@@ -195,8 +195,29 @@ def check_metadata(prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor,
         raise ValueError(f"Bad PrefixLM lengths for sequence {s}: {p} + {c} != {length}")
 
 
+def rope_rows(t: Tensor, T: int, d: int, device, name: str) -> Tensor:
+    """A RoPE table (``cos`` or ``sin``) as float32 rows [T, D] on ``device`` with a
+    unit column stride and 16-byte aligned rows (copied only if needed)."""
+    t = t.reshape(-1, t.shape[-1])
+    if t.shape != (T, d):
+        raise ValueError(f"{name} must hold one [head_dim] row per token: expected {(T, d)}, got {tuple(t.shape)}")
+    if t.device != device or t.dtype != torch.float32 or t.stride(-1) != 1 or t.stride(0) % 4 or t.data_ptr() % 16:
+        t = t.to(device=device, dtype=torch.float32).contiguous()
+    return t
+
+
+def _set_rope(p, rope, T: int, d: int, device) -> tuple:
+    """Point the params' RoPE tables at ``rope`` = (cos, sin); returns the tensors to keep alive."""
+    cos, sin = (rope_rows(t, T, d, device, name) for t, name in zip(rope, ("cos", "sin")))
+    if cos.stride(0) != sin.stride(0):
+        cos, sin = cos.contiguous(), sin.contiguous()
+    p.rope_cos, p.rope_sin, p.rope_stride_token = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+    return cos, sin
+
+
 def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
-                softmax_scale, gate=None, gated_out=None, out_lo=None, split_mode=None, split_flag=None):
+                softmax_scale, gate=None, gated_out=None, out_lo=None, split_mode=None, split_flag=None, rope=None,
+                q_rope=None):
     """Validate, allocate O / lse and fill the C parameter struct of the forward.
 
     Returns ``(params, out, lse, keep)``; ``keep`` holds every tensor the struct
@@ -208,6 +229,9 @@ def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_
     ``split_mode`` is a ``_capi.SPLIT_*`` mode (default: :func:`set_split_mode`);
     with ``split_flag`` (int32 [1], caller-allocated) the launch records its split
     decision there and writes ``out_lo`` only when it splits.
+    With ``rope`` = (cos, sin) (float32 [T, D], bf16 only) the kernel rotates q as
+    it loads it (``k`` must already be rotated) and, given ``q_rope`` ([T, Hq, D],
+    caller-allocated), writes the rotated q there for the backward.
     """
     for name, t in (("q", q), ("k", k), ("v", v)):
         _check_device_tensor(name, t)
@@ -249,6 +273,12 @@ def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_
         _gate_operand("out_lo", out_lo, (T, hq, d), q.dtype, copy=False)
         p.out_lo, p.out_lo_stride_token, p.out_lo_stride_head = out_lo.data_ptr(), out_lo.stride(0), out_lo.stride(1)
         keep = keep + (out_lo,)
+    if rope is not None:
+        keep = keep + _set_rope(p, rope, T, d, device)
+        if q_rope is not None:
+            _gate_operand("q_rope", q_rope, (T, hq, d), q.dtype, copy=False)
+            p.q_rope, p.q_rope_stride_token, p.q_rope_stride_head = q_rope.data_ptr(), q_rope.stride(0), q_rope.stride(1)
+            keep = keep + (q_rope,)
     return p, out, lse, keep
 
 
@@ -290,7 +320,7 @@ def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_se
 
 def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
                 max_seqlen_all, softmax_scale, gate=None, dgate=None, dq=None, dk=None, dv=None, out_lo=None,
-                split_mode=None, split_flag=None):
+                split_mode=None, split_flag=None, rope=None):
     """Validate, allocate dQ / dK / dV and the workspace, fill the backward struct.
 
     Returns ``(params, dq, dk, dv, keep)``.  With ``gate``, ``dout`` is the
@@ -300,6 +330,8 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
     ``out_lo`` is the forward's low output half (bf16), ``split_mode`` a
     ``_capi.SPLIT_*`` mode (default: :func:`set_split_mode`), ``split_flag`` the
     forward's recorded split decision (then followed instead of scanning K).
+    With ``rope`` = (cos, sin) (bf16 only), ``q`` / ``k`` are the rotated operands
+    the forward used and dQ / dK come back as gradients of the unrotated q / k.
 
     The workspace holds the score-gradient hand-off region when it fits the
     limit (:func:`set_dscore_workspace_limit`); if that allocation runs out of
@@ -353,6 +385,8 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
     if split_flag is not None and split_flag.numel() > 0:
         p.split_flag = split_flag.data_ptr()
         gate_keep = gate_keep + (split_flag,)
+    if rope is not None:
+        gate_keep = gate_keep + _set_rope(p, rope, T, d, device)
     p.dscore_limit_bytes = _dscore_limit_bytes
     ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p)))
     try:

@@ -230,6 +230,28 @@ def test_low_half_and_split_mode_validation(lib):
     assert b"split_mode" in lib.mimir_prefixlm_last_error()
 
 
+def test_rope_table_validation(lib):
+    """RoPE inside the kernels: bf16 only, cos and sin together, aligned float32 rows of at least
+    head_dim, and q_rope only with the tables.  All rejected before any launch."""
+    ops = dict(q=16, k=16, v=16, out=16, q_stride_token=512, q_stride_head=128, k_stride_token=256,
+               k_stride_head=128, v_stride_token=256, v_stride_head=128, out_stride_token=512, out_stride_head=128,
+               prefix_lens=16, cu_seqlens=16, workspace=16, workspace_bytes=1 << 20)
+    cases = [
+        (dict(dtype=_capi.DTYPE_FLOAT32, rope_cos=16, rope_sin=32, rope_stride_token=128),
+         _capi.ERR_UNSUPPORTED_DTYPE, b"bfloat16 only"),
+        (dict(rope_cos=16, rope_stride_token=128), _capi.ERR_INVALID_ARGUMENT, b"go together"),
+        (dict(rope_cos=16, rope_sin=36, rope_stride_token=128), _capi.ERR_INVALID_ARGUMENT, b"16-byte aligned"),
+        (dict(rope_cos=16, rope_sin=32, rope_stride_token=64), _capi.ERR_INVALID_ARGUMENT, b"at least head_dim"),
+        (dict(rope_cos=16, rope_sin=32, rope_stride_token=130), _capi.ERR_INVALID_ARGUMENT, b"multiple of 4"),
+        (dict(q_rope=16, q_rope_stride_token=512, q_rope_stride_head=128), _capi.ERR_INVALID_ARGUMENT,
+         b"q_rope needs"),
+    ]
+    for extra, code, msg in cases:
+        p = _fwd(**ops, **extra)
+        assert lib.mimir_prefixlm_fwd(ctypes.byref(p), None) == code, extra
+        assert msg in lib.mimir_prefixlm_last_error(), (extra, lib.mimir_prefixlm_last_error())
+
+
 def test_unknown_backward_stage_bits(lib):
     p = _capi.BwdParams()
     assert lib.mimir_prefixlm_bwd_stages(ctypes.byref(p), 64, None) == _capi.ERR_INVALID_ARGUMENT

@@ -123,3 +123,68 @@ def test_gate_leaves_attention_output_unchanged(device):
           f"mismatching elements {(diff > 0).sum().item()} of {diff.numel()}", flush=True)
     assert diff.max().item() <= 2 ** -7 * y_ref.float().abs().max().item()
     assert (diff > 0).float().mean().item() < 1e-3
+
+
+FUSED = [
+    # seq_lens, prefixes, hq, hkv, d, total_seqlen (None: all)
+    ([190, 64, 3], [64, 64, 0], 8, 2, 128, None),
+    ([300, 257], [0, 100], 4, 4, 64, None),
+    ([300, 500], [50, 100], 8, 2, 128, 300 + 250),  # total_seqlen inside the second sequence
+]
+
+
+@pytest.mark.parametrize("where", [("fwd", "bwd"), ("fwd",), ("bwd",), ()], ids=["fwd+bwd", "fwd", "bwd", "passes"])
+@pytest.mark.parametrize("idx", range(len(FUSED)))
+def test_fused_rope_matches_separate_passes(device, idx, where, monkeypatch):
+    """bf16 RoPE inside the kernels (q rotated as the forward loads it, dQ / dK mapped back in
+    the backward's stores), and the layer's merged passes, against the separate per-tensor
+    passes: rope(q), rope(k), the attention, and rope's inverse on dQ / dK.  Same operands bit
+    for bit, hence the same y, gqkv gradient and rotated-q copy bit for bit."""
+    monkeypatch.setattr(L, "_ROPE_IN_KERNELS", frozenset(where))
+    seq_lens, prefixes, hq, hkv, d, total = FUSED[idx]
+    case = make_case(seq_lens, prefixes, hq, hkv, d, dtype=torch.bfloat16, seed=50 + idx)
+    if total is not None:
+        case.total_seqlen = torch.tensor(total, dtype=torch.int64)
+    T = case.T
+    gen = torch.Generator().manual_seed(60 + idx)
+    gqkv = torch.randn(T, (2 * hq + 2 * hkv) * d, generator=gen).to(torch.bfloat16).to(device)
+    dy = torch.randn(T, hq * d, generator=gen).to(torch.bfloat16).to(device)
+    cos, sin = (t.to(device) for t in _cos_sin(_positions(seq_lens, T), d))
+    c = case.to(device)
+    meta = dict(prefix_lens=c.prefix_lens, causal_lens=c.causal_lens, cu_seqlens=c.cu_seqlens,
+                total_seqlen=c.total_seqlen, numseqs=c.numseqs, max_seqlen_all=c.max_seqlen_all)
+
+    g1 = gqkv.clone().requires_grad_(True)
+    y1 = L.gated_attention(g1, (cos, sin), hq, hkv, False, **meta)
+    y1.backward(dy)
+
+    g3 = gqkv.view(T, -1, d)
+    rot = g3.clone()
+    rot[:, hq:2 * hq] = L.rope(g3[:, hq:2 * hq], cos, sin)
+    rot[:, 2 * hq:2 * hq + hkv] = L.rope(g3[:, 2 * hq:2 * hq + hkv], cos, sin)
+    g2 = rot.reshape(T, -1).requires_grad_(True)
+    y2 = L.gated_attention(g2, None, hq, hkv, False, **meta)
+    y2.backward(dy)
+    dg2 = g2.grad.view(T, -1, d).clone()
+    dg2[:, hq:2 * hq] = L.rope(dg2[:, hq:2 * hq], cos, sin, inverse=True)
+    dg2[:, 2 * hq:2 * hq + hkv] = L.rope(dg2[:, 2 * hq:2 * hq + hkv], cos, sin, inverse=True)
+    torch.cuda.synchronize()
+    dg1 = g1.grad.view(T, -1, d)
+    print(f"[fused rope] case{idx} {where} d={d} y mismatches {(y1 != y2).sum().item()}, "
+          f"grad mismatches {(dg1 != dg2).sum().item()}", flush=True)
+    assert torch.equal(y1, y2)
+    assert torch.equal(dg1, dg2)
+
+    # the rotated q the forward writes for the backward: rope(q) on every active row
+    q = g3[:, hq:2 * hq]
+    q_rope = torch.full((T, hq, d), float("nan"), dtype=torch.bfloat16, device=device)
+    k_rope = L.rope(g3[:, 2 * hq:2 * hq + hkv], cos, sin)
+    p, o, lse, keep = P.prepare_fwd(q, k_rope, g3[:, 2 * hq + hkv:], False, c.prefix_lens, c.causal_lens,
+                                    c.cu_seqlens, c.total_seqlen, c.numseqs, c.max_seqlen_all, d ** -0.5,
+                                    rope=(cos, sin), q_rope=q_rope)
+    import ctypes
+    lib = P._capi.load()
+    P._capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), P._stream(device)))
+    torch.cuda.synchronize()
+    active = int(c.total_seqlen) if total is not None else sum(seq_lens)
+    assert torch.equal(q_rope[:active], L.rope(q, cos, sin)[:active])
