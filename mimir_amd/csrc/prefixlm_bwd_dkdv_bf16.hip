@@ -275,7 +275,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
       for (int e = 0; e < 4; ++e) tv[e] = dvacc[dt][4 * rg + e];
       *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
     }
-  grad_out<DT>(dkacc, a.scale, rope_args(a.rope), g.start + kpos, hi,
+  grad_out<DT>(dkacc, a.scale, a.rope, g.start + kpos, hi,
                [&](int dt, int rg, bf16x4 v) { *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = v; });
 }
 

@@ -265,8 +265,12 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     __amdgpu_buffer_rsrc_t rds;
     if constexpr (kStoreDs) {
       const int row = ds_row0 + (qr >> 5);
-      const int64_t blk = ((int64_t)(hk * a.group + head) * a.ds_rows + row) * a.ds_width + (ka >> 5);
-      rds = make_rsrc(a.dscore + blk * kDsBlockElems, ds_unit_ok ? kDsBlockElems * 2 : 0);
+      // region geometry loaded per step: no scalar registers held across the loop
+      const int64_t blk = ((int64_t)(hk * a.group + head) * kernarg_at<int>(offsetof(BwdArgs, ds_rows)) + row) *
+                              kernarg_at<int>(offsetof(BwdArgs, ds_width)) +
+                          (ka >> 5);
+      rds = make_rsrc(kernarg_at<bf16_t*>(offsetof(BwdArgs, dscore)) + blk * kDsBlockElems,
+                      ds_unit_ok ? kDsBlockElems * 2 : 0);
     }
     auto store_ds = [&](int s2) {
       if constexpr (kStoreDs)
@@ -390,8 +394,10 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     constexpr int kDevScope = 16;  // buffer cache policy: coherent at device scope
     constexpr uint32_t kSliceBytes = DT * 4 * 64 * 16;
     const int ph = item.w * a.Hkv + hk;
-    const float* const slot_mine = a.split_buf + ((size_t)ph * 2 + (half - 1)) * kSplitSlotFloats;
-    const float* const slot_other = a.split_buf + ((size_t)ph * 2 + (2 - half)) * kSplitSlotFloats;
+    float* const split_buf = kernarg_at<float*>(offsetof(BwdArgs, split_buf));
+    int* const split_ctr = kernarg_at<int*>(offsetof(BwdArgs, split_ctr));
+    const float* const slot_mine = split_buf + ((size_t)ph * 2 + (half - 1)) * kSplitSlotFloats;
+    const float* const slot_other = split_buf + ((size_t)ph * 2 + (2 - half)) * kSplitSlotFloats;
     if (qh == 0) {
       const __amdgpu_buffer_rsrc_t rs = make_rsrc(slot_mine, kSplitSlotFloats * 4);
 #pragma unroll
@@ -410,8 +416,8 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     }
     __syncthreads();
     if (tid == 0) {
-      const int prev = __hip_atomic_fetch_add(&a.split_ctr[ph], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (prev == 1) __hip_atomic_store(&a.split_ctr[ph], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int prev = __hip_atomic_fetch_add(&split_ctr[ph], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (prev == 1) __hip_atomic_store(&split_ctr[ph], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       later = prev;
     }
     __syncthreads();
@@ -447,8 +453,13 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   if (qh != 0 || !wave_active) return;
   const int kpos = ka + l32;
   if (kpos >= g.n) return;
-  bf16_t* krow = a.dk + (int64_t)(g.start + kpos) * a.dk_st + (int64_t)hk * a.dk_sh;
-  bf16_t* vrow = a.dv + (int64_t)(g.start + kpos) * a.dv_st + (int64_t)hk * a.dv_sh;
+  // the destinations loaded here: no scalar registers held across the tile loop
+  bf16_t* krow = kernarg_at<bf16_t*>(offsetof(BwdArgs, dk)) +
+                 (int64_t)(g.start + kpos) * kernarg_at<int64_t>(offsetof(BwdArgs, dk_st)) +
+                 (int64_t)hk * kernarg_at<int64_t>(offsetof(BwdArgs, dk_sh));
+  bf16_t* vrow = kernarg_at<bf16_t*>(offsetof(BwdArgs, dv)) +
+                 (int64_t)(g.start + kpos) * kernarg_at<int64_t>(offsetof(BwdArgs, dv_st)) +
+                 (int64_t)hk * kernarg_at<int64_t>(offsetof(BwdArgs, dv_sh));
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -458,7 +469,8 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
       for (int e = 0; e < 4; ++e) tv[e] = dvacc[dt][4 * rg + e];
       *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
     }
-  grad_out<DT>(dkacc, a.scale, rope_args(a.rope), g.start + kpos, hi,
+  grad_out<DT>(dkacc, kernarg_at<float>(offsetof(BwdArgs, scale)), rope_at(offsetof(BwdArgs, rope)),
+               g.start + kpos, hi,
                [&](int dt, int rg, bf16x4 v) { *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = v; });
   };
 

@@ -5,6 +5,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include <string>
@@ -59,6 +60,9 @@ struct SeqGeom {
 // prefix tiles pile up on half of the XCDs.  An odd width rotates each row by
 // one XCD; the padding column exits at once.
 inline unsigned xcd_spread_width(int n) { return (unsigned)(n | 1); }
+// XCDs of an MI355X in SPX mode: workgroup b of a launch runs on XCD b % kXcds
+// (measured: the XCC_ID hardware register of every workgroup).
+constexpr int kXcds = 8;
 
 // Sequence bounds are clamped to the packed length T so that malformed metadata
 // can never address memory outside the [T, ...] tensors.
@@ -190,11 +194,22 @@ struct RopeTab {
   int64_t st;        // elements between the rows of cos / sin
 };
 
-// The tables re-read from the kernel arguments where they are used (a volatile
-// read cannot be hoisted), so that they hold no scalar registers across a tile loop.
-__device__ __forceinline__ RopeTab rope_args(const RopeTab& r) {
-  const volatile RopeTab* p = &r;
-  return RopeTab{p->cos, p->sin, p->st};
+// A field of the kernel's argument struct (the kernel's only parameter, at the
+// start of the kernarg segment), loaded where it is used: the segment pointer
+// is opaque to the compiler, so the scalar load is not hoisted and the value
+// holds no scalar registers across a tile loop (where it would be spilled).
+template <typename T>
+__device__ __forceinline__ T kernarg_at(size_t offset) {
+  typedef const __attribute__((address_space(4))) char* KPtr;
+  KPtr p = (KPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  __asm__ volatile("" : "+s"(p));
+  return *(const __attribute__((address_space(4))) T*)(p + offset);
+}
+// The RoPE tables of the argument struct at `offset`, loaded the same way.
+__device__ __forceinline__ RopeTab rope_at(size_t offset) {
+  return RopeTab{kernarg_at<const float*>(offset + offsetof(RopeTab, cos)),
+                 kernarg_at<const float*>(offset + offsetof(RopeTab, sin)),
+                 kernarg_at<int64_t>(offset + offsetof(RopeTab, st))};
 }
 
 // Rotation of four column pairs (d1 + e, d1 + e + half), e < 4, of token t.
