@@ -241,7 +241,9 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* params, void* stream);
  * race; the array needs no clearing between calls.  Outputs as mimir_prefixlm_fwd. */
 int mimir_prefixlm_fwd_noalloc(const MimirPrefixLMFwdParams* params, void* stream);
 
-/* Backward: dq, dk, dv from dout, out and lse.  Deterministic and atomic-free.
+/* Backward: dq, dk, dv from dout, out and lse.  Deterministic: every gradient
+ * element is summed in a fixed order by one owner (atomics only count work-queue
+ * units and split-tile arrivals).
  * Replaces the FA3 backward custom op src/mimir/model/flash_attention_prefixlm_v2.py:165-227,
  * FA4's backward reached through fa4.py:153-179,309-331, and the Metal split
  * backward src/mimir/model/flash_attention_prefixlm_mps.py:1456-1561. */

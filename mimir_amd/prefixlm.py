@@ -83,8 +83,11 @@ def set_dscore_workspace_limit(nbytes: int) -> None:
     With bf16 and head_dim 128 the dK / dV kernel can hand its bf16 dS tiles to
     the dQ kernel, which then computes dQ = dS K without recomputing S and dP.
     The tiles take ``Hq * (T / 32 + numseqs + 1) * ceil(max_seqlen / 32) * 2 KiB``
-    (about 1.1 GB for 8 x 2048 tokens and 16 heads); above this limit the dQ
-    kernel recomputes instead.  0 turns the hand-off off.  Default 4 GiB.
+    (about 1.1 GB for 8 x 2048 tokens and 16 heads); above this limit, or (for
+    a region above 1/64 of the device's memory) above half of the device memory
+    free at the call (what the driver reports plus torch's cached free blocks),
+    the dQ kernel recomputes instead; and if the allocation still fails, the
+    backward retries without the tiles.  0 turns the hand-off off.  Default 4 GiB.
     """
     global _dscore_limit_bytes
     if nbytes < 0:
@@ -388,6 +391,9 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
     if rope is not None:
         gate_keep = gate_keep + _set_rope(p, rope, T, d, device)
     p.dscore_limit_bytes = _dscore_limit_bytes
+    region = int(lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p))) if _dscore_limit_bytes > 0 else 0
+    if region > _total_device_bytes(device) // 64:  # a large region: keep it to half of what is free
+        p.dscore_limit_bytes = min(_dscore_limit_bytes, _free_device_bytes(device) // 2)
     ws_bytes = int(lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p)))
     try:
         ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
@@ -400,6 +406,24 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
         ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
     p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
     return p, dq, dk, dv, (q, k, v, out, dout, lse, pl, cl, cu, ws) + gate_keep
+
+
+_total_bytes = {}
+
+
+def _total_device_bytes(device) -> int:
+    """The device's memory size (cached per device)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _total_bytes:
+        _total_bytes[idx] = int(torch.cuda.get_device_properties(idx).total_memory)
+    return _total_bytes[idx]
+
+
+def _free_device_bytes(device) -> int:
+    """Device memory an allocation can still get: free in the driver plus torch's cached free blocks.
+    (A few hundred microseconds of host time: asked only for regions above 1/64 of the device.)"""
+    free, _total = torch.cuda.mem_get_info(device)
+    return int(free) + int(torch.cuda.memory_reserved(device)) - int(torch.cuda.memory_allocated(device))
 
 
 def _bwd_impl(dout, q, k, v, out, lse, out_lo, split_flag, is_causal, prefix_lens, causal_lens, cu_seqlens,

@@ -9,6 +9,8 @@ Tolerances (max-abs, written here as the contract):
   fp32 kernel:  O <= 1e-5, lse <= 1e-5; fp32 gradients <= 1e-4
 """
 
+import ctypes
+
 import pytest
 import torch
 
@@ -373,3 +375,48 @@ def test_workspace_oom_falls_back_to_recompute(device, monkeypatch):
     assert torch.equal(got["dk"], base["dk"]) and torch.equal(got["dv"], base["dv"])
     assert (got["dq"] - base["dq"]).abs().max().item() <= 1e-2
     check(case, device, label="after OOM fallback")
+
+
+def test_dscore_region_bounded_by_free_memory(device, monkeypatch):
+    """A large score-gradient region is requested only while it fits half of the free device
+    memory: with the free memory reported just below twice the region the backward allocates
+    the small workspace and recomputes dQ (dK / dV bit for bit, dQ within the bar); just above
+    it, the workspace holds the region and dQ is the hand-off's, bit for bit."""
+    from mimir_amd import prefixlm as P
+    from mimir_amd import _capi
+
+    case = make_case([900, 333], [450, 0], 8, 2, 128, seed=52, dtype=torch.bfloat16)
+    lib = _capi.load()
+    b = _capi.BwdParams()
+    b.total_tokens, b.num_q_heads, b.num_kv_heads, b.numseqs, b.max_seqlen_all = case.T, 8, 2, 2, 900
+    b.head_dim, b.dtype, b.dscore_limit_bytes = 128, _capi.DTYPE_BFLOAT16, 1 << 40
+    region = int(lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(b)))
+    small = int(lib.mimir_prefixlm_bwd_workspace_bytes(case.T, 8, 2, 900))
+    assert region > 0
+    base = run_gpu(case, device)  # hand-off (plenty of free memory)
+    real_empty = torch.empty
+    for free, handoff in ((2 * region - 2, False), (2 * region + 2, True)):
+        requested = []
+
+        def empty(*shape, **kw):
+            if kw.get("dtype") is torch.float32:
+                n = 1
+                for d in (shape[0] if len(shape) == 1 and isinstance(shape[0], (tuple, list)) else shape):
+                    n *= int(d)
+                requested.append(n * 4)
+            return real_empty(*shape, **kw)
+
+        monkeypatch.setattr(P, "_free_device_bytes", lambda dev, f=free: f)
+        monkeypatch.setattr(P, "_total_device_bytes", lambda dev: 0)  # every region counts as large
+        monkeypatch.setattr(P.torch, "empty", empty)
+        got = run_gpu(case, device)
+        monkeypatch.undo()
+        ws = max(requested)
+        print(f"[free-memory bound] free {free} region {region}: workspace {ws} (small {small})", flush=True)
+        assert (ws > small + region // 2) == handoff
+        assert torch.equal(got["dk"], base["dk"]) and torch.equal(got["dv"], base["dv"])
+        if handoff:
+            assert torch.equal(got["dq"], base["dq"])
+        else:
+            assert (got["dq"] - base["dq"]).abs().max().item() <= 1e-2
+    check(case, device, label="free-memory bound")
