@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MIMIR_PREFIXLM_ABI_VERSION 6
+#define MIMIR_PREFIXLM_ABI_VERSION 7
 
 /* Element types of q/k/v/out/dout/dq/dk/dv (lse and the workspace are float32). */
 enum MimirDType {
@@ -216,11 +216,26 @@ typedef struct MimirPrefixLMBwdParams {
 } MimirPrefixLMBwdParams;
 
 /* Bytes of device workspace the forward needs: the heaviest-first tile work list
- * (int32 pairs, one per 128-row query tile of every sequence; sized
+ * (16-byte entries, one per 128-row query tile of every sequence; sized
  * ceil(T / 128) + numseqs, which bounds the tiles of any packing of T tokens into
  * numseqs sequences, so it does not rely on max_seqlen_all), then, 256-byte
  * aligned, the 512 int32 slots of the K scan behind split_mode AUTO. */
 size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs, int32_t max_seqlen_all);
+
+/* Bytes of device workspace with which the bf16 forward may also cut the key
+ * ranges of its heaviest query tiles into parts (at most 16 per tile), run
+ * them as separate workgroups and merge their partial outputs in part order
+ * (deterministic): on a small grid -- fewer than 512 (query tile, q head)
+ * workgroups -- the heaviest tiles otherwise run alone on a few compute units
+ * at the end.  No counterpart in the reference (an extension of the forward's
+ * own scheduling).  It adds 1024 / num_q_heads chunk slots of
+ * (4 * head_dim * 128 + 2048) bytes per q head and their arrival counters; it
+ * equals mimir_prefixlm_fwd_workspace_bytes where the grid cannot be small
+ * (ceil(total_tokens / 128) * num_q_heads >= 512) and for float32.  The forward
+ * cuts key ranges iff its workspace_bytes reaches this size; any size from
+ * mimir_prefixlm_fwd_workspace_bytes up is valid.  Reads only dtype,
+ * total_tokens, num_q_heads, head_dim, numseqs and max_seqlen_all. */
+size_t mimir_prefixlm_fwd_workspace_size(const MimirPrefixLMFwdParams* params);
 
 /* Forward: out (and lse if non-NULL).
  * Replaces the FA4 two-pass forward, src/mimir/model/flash_attention_prefixlm_fa4.py:353-406
@@ -236,7 +251,7 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* params, void* stream);
  * library (one per GPU, held until the process ends): a call whose
  * mimir_prefixlm_fwd_workspace_bytes exceeds 128 KiB fails with
  * MIMIR_ERR_UNSUPPORTED_SHAPE before any device work (it fits while
- * ceil(total_tokens / 128) + numseqs <= 16128).  It calls no hipMalloc / hipFree.  Every call on one GPU
+ * ceil(total_tokens / 128) + numseqs <= 8064); it never cuts key ranges.  It calls no hipMalloc / hipFree.  Every call on one GPU
  * shares that array, so calls that overlap on one GPU (two streams or threads)
  * race; the array needs no clearing between calls.  Outputs as mimir_prefixlm_fwd. */
 int mimir_prefixlm_fwd_noalloc(const MimirPrefixLMFwdParams* params, void* stream);

@@ -16,7 +16,7 @@ from pathlib import Path
 
 # MIMIR_PREFIXLM_LIB overrides the in-tree library (e.g. to A/B two builds).
 LIB_PATH = Path(os.environ.get("MIMIR_PREFIXLM_LIB") or Path(__file__).resolve().parent / "_lib" / "libmimir_prefixlm.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_FLOAT32 = 0
 DTYPE_BFLOAT16 = 1
@@ -124,6 +124,7 @@ EXPORTED_SYMBOLS = (
     "mimir_prefixlm_bwd",
     "mimir_prefixlm_bwd_stages",
     "mimir_prefixlm_fwd_workspace_bytes",
+    "mimir_prefixlm_fwd_workspace_size",
     "mimir_prefixlm_bwd_workspace_bytes",
     "mimir_prefixlm_bwd_workspace_size",
     "mimir_prefixlm_bwd_dscore_bytes",
@@ -167,6 +168,8 @@ def load() -> ctypes.CDLL:
         lib.mimir_prefixlm_bwd_stages.restype = ctypes.c_int
         lib.mimir_prefixlm_fwd_workspace_bytes.argtypes = [_i32, _i32, _i32]
         lib.mimir_prefixlm_fwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.mimir_prefixlm_fwd_workspace_size.argtypes = [ctypes.POINTER(FwdParams)]
+        lib.mimir_prefixlm_fwd_workspace_size.restype = ctypes.c_size_t
         lib.mimir_prefixlm_bwd_workspace_bytes.argtypes = [_i32, _i32, _i32, _i32]
         lib.mimir_prefixlm_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.mimir_prefixlm_bwd_workspace_size.argtypes = [ctypes.POINTER(BwdParams)]

@@ -132,7 +132,19 @@ int mimir_prefixlm_abi_version(void) { return MIMIR_PREFIXLM_ABI_VERSION; }
 size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs, int32_t max_seqlen_all) {
   const int cap = mimir::plan_capacity(total_tokens, numseqs, max_seqlen_all);
   if (cap <= 0) return 0;
-  return mimir::fwd_kscan_offset(cap) + (size_t)mimir::kKScanSlots * sizeof(int);
+  return mimir::fwd_workspace_layout(cap, 0, 0, false).total;
+}
+
+size_t mimir_prefixlm_fwd_workspace_size(const MimirPrefixLMFwdParams* p) {
+  if (p == nullptr) return 0;
+  const size_t base = mimir_prefixlm_fwd_workspace_bytes(p->total_tokens, p->numseqs, p->max_seqlen_all);
+  // key-range parts: bf16 only, and only where the grid can be small (a list of
+  // at least ceil(T / 128) query tiles per q head fills kFwdChunkWgs otherwise)
+  if (base == 0 || p->dtype != MIMIR_DTYPE_BFLOAT16 || p->num_q_heads <= 0 || p->head_dim <= 0) return base;
+  const int64_t tiles = ((int64_t)p->total_tokens + mimir::kPlanTile - 1) / mimir::kPlanTile;
+  if (tiles * p->num_q_heads >= mimir::kFwdChunkWgs) return base;
+  const int cap = mimir::plan_capacity(p->total_tokens, p->numseqs, p->max_seqlen_all);
+  return mimir::fwd_workspace_layout(cap, p->num_q_heads, p->head_dim, true).total;
 }
 
 size_t mimir_prefixlm_bwd_dscore_bytes(const MimirPrefixLMBwdParams* p) {

@@ -437,15 +437,18 @@ constexpr int kPlanTile = 128;
 // sum_s ceil(n_s / 128) <= ceil(T / 128) + numseqs.  max_seqlen_all is not used,
 // so metadata with an understated max_seqlen_all still lists every tile.
 int plan_capacity(int total_tokens, int numseqs, int max_seqlen_all);
-// Forward workspace: the work list (int2 [cap]), then at this 256-byte aligned
-// offset the kKScanSlots int32 slots of the K scan.
-inline size_t fwd_kscan_offset(int cap) { return ((size_t)(cap > 0 ? cap : 0) * 8 + 255) & ~(size_t)255; }
+
 
 struct PlanArgs {
   const int32_t* cu_seqlens;
   const int32_t* prefix_lens;
   int numseqs, total_seqlen, is_causal, T, kind, group, cap;
-  void* items;     // int2 [cap] (kind 0) or int4 [cap] (kind 1)
+  void* items;     // int2 [cap] (kind 0) or int4 [cap] (kinds 1 and 2)
+  // kind 2 (the forward's query tiles, int4 (sequence, tile, part | parts << 16,
+  // chunk slot)): when the grid is small (items * split_heads < slots) the key
+  // range of every item costing more than (total cost * split_heads / slots,
+  // at least kFwdChunkMinCost) is cut into parts of about that cost, at most
+  // kFwdChunkMax; max_pairs (the chunk slots available) = 0 disables it.
   // kind 1: split items costing more than (total cost * split_heads / slots) / 2,
   // heaviest first and whole cost buckets at a time, up to max_pairs items;
   // split_heads = 0 disables splitting.
@@ -471,6 +474,40 @@ constexpr int kSplitSlotFloats = 2 * 128 * 128;   // dK + dV partial of one part
 // kernel could not store a score-gradient tile (a sequence longer than
 // max_seqlen_all), so that the recomputing dQ kernel takes over from the hand-off.
 constexpr int kKScanSlots = 512;
+
+// Key-range chunks of the forward (kind-2 list): small grids leave most CUs idle
+// while the heaviest query tiles run, so their key ranges are cut into parts
+// that run as separate workgroups and are merged by the last to finish.
+constexpr int kFwdChunkMax = 16;        // parts per query tile
+constexpr int kFwdChunkMinCost = 4;     // key tiles per part, at least
+constexpr int kFwdChunkWgs = 512;       // forward workgroups resident at once (2 per CU)
+constexpr int kFwdChunkHeadSlots = 2 * kFwdChunkWgs;  // chunk slots x q heads, at most
+// Chunk slots for Hq heads: with parts cut at the per-workgroup average cost
+// of one round, the parts of the split tiles number at most 2 * kFwdChunkWgs / Hq.
+inline int fwd_chunk_slots(int hq) { return hq > 0 ? kFwdChunkHeadSlots / hq : 0; }
+// One chunk slot per (part, q head): the part's unnormalized O (fp32, per wave
+// DT * 4 float4 per lane, lane-major) then its running max and sum per lane.
+__host__ __device__ inline size_t fwd_chunk_slot_bytes(int d) { return (size_t)4 * (size_t)d * 128 + (size_t)4 * 64 * 8; }
+// Forward workspace, 256-byte aligned sections: the work list (int4 [cap +
+// chunk slots]), the kKScanSlots int32 slots of the K scan, then with chunking
+// one arrival counter per (chunk slot, q head) and the chunk slots.
+struct FwdWorkspace {
+  size_t list, kscan, ctr, part, total;
+  int list_cap, chunk_slots;
+};
+inline FwdWorkspace fwd_workspace_layout(int cap, int hq, int d, bool chunks) {
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  FwdWorkspace w;
+  w.chunk_slots = chunks && cap > 0 ? fwd_chunk_slots(hq) : 0;
+  w.list_cap = cap > 0 ? cap + w.chunk_slots : 0;
+  w.list = 0;
+  w.kscan = align((size_t)w.list_cap * 16);
+  w.ctr = align(w.kscan + (size_t)kKScanSlots * sizeof(int));
+  w.part = align(w.ctr + (size_t)w.chunk_slots * (size_t)(hq > 0 ? hq : 0) * sizeof(int));
+  w.total = w.chunk_slots > 0 ? w.part + (size_t)w.chunk_slots * (size_t)hq * fwd_chunk_slot_bytes(d)
+                              : w.ctr;
+  return w;
+}
 constexpr float kSplitThreshold = 0.75f;
 constexpr int kCounterWordsAfterPairs = 3;  // work queue next / finished, dS-incomplete flag
 

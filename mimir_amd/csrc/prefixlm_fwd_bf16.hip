@@ -44,7 +44,7 @@ struct FwdArgs {
   int group;         // Hq / Hkv
   int total_seqlen;
   int is_causal;
-  const int2* plan;  // (sequence, query tile) per workgroup row, heaviest first (prefixlm_prologue.hip)
+  const int4* plan;  // (sequence, query tile, part | parts << 16, chunk slot), heaviest first (prefixlm_prologue.hip)
   int cap;           // entries of the list
   float scale;       // softmax scale
   float scale_log2;  // softmax scale * log2(e)
@@ -56,27 +56,48 @@ struct FwdArgs {
   const int* kscan;    // the prologue's K scan (split_mode AUTO)
   int split_mode;      // MimirSplitMode: P as bf16 hi + lo in O^T += V^T P^T
   int* split_flag;     // optional: the decision, for the backward
+  int* chunk_ctr;      // arrival counter per (first chunk slot of a tile, q head)
+  char* chunk_part;    // partials per (chunk slot, q head), fwd_chunk_slot_bytes(D) each
   RopeTab rope;        // optional RoPE of Q, applied to the loaded fragments
   bf16_t* q_rope;      // optional: the rotated Q rows, for the backward
   int64_t qr_st, qr_sh;
 };
 
+// Two LDS stages of one K tile and one V tile each.  Separate objects let the
+// compiler see that reads of one stage never alias the loads into the other;
+// declared apart from the tile loop's body so that both of a kernel's bodies
+// (split and plain P) use the same LDS.
+template <int D>
+struct FwdStages {
+  bf16_t *k0, *v0, *k1, *v1;
+};
+template <int D>
+__device__ __forceinline__ FwdStages<D> fwd_stages() {
+  using L = TileLayout<D>;
+  __shared__ __attribute__((aligned(16))) bf16_t sK0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV0[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sK1[L::kElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV1[L::kElems];
+  return FwdStages<D>{sK0, sV0, sK1, sV1};
+}
+
 // kSplit: P is not (0) / is (1) split.  The split changes the registers of the
 // tile loop, so it is a compile-time choice: split_mode AUTO enqueues both
-// instantiations and the one the K scan does not select exits at once.
+// instantiations and the one the K scan does not select exits at once.  (One
+// kernel holding both bodies behind a uniform branch was measured: with the two
+// bodies in one function the plain one ran 10-17% slower.)
 template <int D, int kGated, int kSplit>
 __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   constexpr int DT = D / 32;  // 32-row d tiles of O^T
   constexpr int KS = D / 16;  // k-steps of S^T = K Q^T
 
-  // Two LDS stages of one K tile and one V tile each.  Separate objects let the
-  // compiler see that reads of one stage never alias the loads into the other.
   using L = TileLayout<D>;
   static_assert(kBlockN == 64, "one TileLayout tile per K / V block");
-  __shared__ __attribute__((aligned(16))) bf16_t sK0[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sV0[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sK1[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sV1[L::kElems];
+  const FwdStages<D> stages = fwd_stages<D>();
+  bf16_t* const sK0 = stages.k0;
+  bf16_t* const sV0 = stages.v0;
+  bf16_t* const sK1 = stages.k1;
+  bf16_t* const sV1 = stages.v1;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -100,10 +121,11 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   if (unit >= a.cap * hkv) return;
   const int rank = unit / hkv;
   const int h = (unit - rank * hkv) * a.group + slot % a.group;
-  const int2 item = a.plan[rank];
+  const int4 item = a.plan[rank];
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int mtile = item.y;
+  const int part = item.z & 0xffff, parts = item.z >> 16;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = mtile * kBlockM;
   if (m0 >= g.nq) return;
@@ -111,7 +133,10 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
 
   const int wg_qend = min(m0 + kBlockM, g.nq);
   const int wg_kend = max(g.p, wg_qend);
-  const int nkt = (wg_kend + kBlockN - 1) / kBlockN;
+  const int nkt_all = (wg_kend + kBlockN - 1) / kBlockN;
+  // key tiles [kt0, kt1) of this part (the whole range unless the list cut it)
+  const int kt0 = (int)((int64_t)part * nkt_all / parts);
+  const int nkt = (int)((int64_t)(part + 1) * nkt_all / parts);
 
   const int qa = m0 + wave * 32;
   const bool wave_active = qa < g.nq;
@@ -127,9 +152,9 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   const TileLoader<D, kWaves> ldk(a.k_st, wave, lane), ldv(a.v_st, wave, lane);
 
   // Tile copies walk the key tiles in order with running addresses (adds only).
-  const bf16_t* i_k = kseq;
-  const bf16_t* i_v = vseq;
-  int i_rows = g.n;
+  const bf16_t* i_k = kseq + (int64_t)kt0 * kBlockN * a.k_st;
+  const bf16_t* i_v = vseq + (int64_t)kt0 * kBlockN * a.v_st;
+  int i_rows = g.n - kt0 * kBlockN;
   auto issue_next = [&](bf16_t* tk, bf16_t* tv) {
     ldk.issue_at(i_k, rows_bytes32(i_rows, (uint32_t)a.k_st, D), tk);
     ldv.issue_at(i_v, rows_bytes32(i_rows, (uint32_t)a.v_st, D), tv);
@@ -137,7 +162,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
     i_v += kBlockN * a.v_st;
     i_rows -= kBlockN;
   };
-  issue_next(sK0, sV0);
+  if (kt0 < nkt) issue_next(sK0, sV0);
 
   // Q^T B-operand fragments: lane holds query qpos, d = 16*ks + 8*hi .. +7.
   bf16x8 qf[KS];
@@ -235,17 +260,18 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
     // more than 2^8 in probability terms (always on the first tile, where m_run is
     // -inf).  In between, probabilities stay below 256, exact in fp32 and in bf16's
     // range; the final 1/l uses the same reference, so the result is unchanged.
+    // A part of a cut key range can meet a row's masked keys before any visible
+    // one: the row keeps m_run = -inf (alpha 1, probabilities exp2(-inf) = 0).
     const float m_cand = fmaxf(m_run, mx);
     const bool grow = (m_cand - m_run) * c2 > 8.f;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float m_new = grow ? m_cand : m_run;
-      const float alpha = fast_exp2((m_run - m_new) * c2);
+      const float alpha = grow ? fast_exp2((m_run - m_cand) * c2) : 1.f;
       l_run *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-      m_run = m_new;
+      if (grow) m_run = m_cand;
     }
-    const float mb = m_run * c2;
+    const float mb = m_run == -INFINITY ? 0.f : m_run * c2;
 
     float lsum = 0.f;
 #pragma unroll
@@ -290,7 +316,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
     compute(kb + kBlockN > w_kend_min, kt, sK, sV);
   };
 
-  for (int kt = 0; kt < nkt; kt += 2) {
+  for (int kt = kt0; kt < nkt; kt += 2) {
     wait_vmem();
     __syncthreads();
     if (kt + 1 < nkt) issue_next(sK1, sV1);
@@ -300,6 +326,77 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
     __syncthreads();
     if (kt + 2 < nkt) issue_next(sK0, sV0);
     step(kt + 1, sK1, sV1);
+  }
+
+  // A part of a cut key range: publish the partial (unnormalized O, running max
+  // and sum per lane) in its chunk slot; the last part of the tile to arrive
+  // merges all of them, in part order, and runs the epilogue.
+  if (__builtin_expect(parts > 1, 0)) {
+    __shared__ int later;
+    constexpr int kDevScope = 16;  // buffer cache policy: coherent at device scope
+    constexpr uint32_t kOBytes = (uint32_t)D * 128 * 4;
+    const int slot0 = item.w - part;
+    const size_t slot_bytes = fwd_chunk_slot_bytes(D);
+    char* const mine = a.chunk_part + ((size_t)item.w * a.Hq + h) * slot_bytes;
+    {
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(mine, (uint32_t)slot_bytes);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const f32x4 v = {oacc[dt][4 * rg], oacc[dt][4 * rg + 1], oacc[dt][4 * rg + 2], oacc[dt][4 * rg + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), r,
+                                                 (uint32_t)((((wave * DT + dt) * 4 + rg) * 64 + lane) * 16), 0,
+                                                 kDevScope);
+        }
+      const f32x2 ml = {m_run, l_run};
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, ml), r,
+                                            kOBytes + (uint32_t)((wave * 64 + lane) * 8), 0, kDevScope);
+    }
+    __asm__ volatile("" ::: "memory");
+    wait_vmem();  // the slot stores are complete
+    __syncthreads();
+    if (tid == 0) {
+      int* const ctr = a.chunk_ctr + (size_t)slot0 * a.Hq + h;
+      const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (prev == parts - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      later = prev == parts - 1;
+    }
+    __syncthreads();
+    if (!later) return;
+    // Merge: max of the parts' reference maxima, then the sum of their sums and
+    // O accumulators rescaled to it (a part with no key for the row has max -inf).
+    auto slot_of = [&](int q) {
+      return make_rsrc(a.chunk_part + ((size_t)(slot0 + q) * a.Hq + h) * slot_bytes, (uint32_t)slot_bytes);
+    };
+    float m_all = -INFINITY;
+    for (int q = 0; q < parts; ++q) {
+      const i32x2 v = __builtin_amdgcn_raw_buffer_load_b64(slot_of(q), kOBytes + (uint32_t)((wave * 64 + lane) * 8),
+                                                           0, kDevScope);
+      m_all = fmaxf(m_all, __builtin_bit_cast(f32x2, v)[0]);
+    }
+    float l_all = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
+    for (int q = 0; q < parts; ++q) {
+      const __amdgpu_buffer_rsrc_t r = slot_of(q);
+      const f32x2 ml = __builtin_bit_cast(
+          f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, kOBytes + (uint32_t)((wave * 64 + lane) * 8), 0, kDevScope));
+      const float f = ml[0] == -INFINITY ? 0.f : fast_exp2((ml[0] - m_all) * c2);
+      l_all += ml[1] * f;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const f32x4 v = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         r, (uint32_t)((((wave * DT + dt) * 4 + rg) * 64 + lane) * 16), 0, kDevScope));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) oacc[dt][4 * rg + e] += v[e] * f;
+        }
+    }
+    m_run = m_all;
+    l_run = l_all;
   }
 
   // Epilogue: each wave stages its 32 output rows (and the gated rows) in LDS --
@@ -443,14 +540,29 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t str
   a.q_rope = (bf16_t*)p.q_rope;
   a.qr_st = p.q_rope_stride_token; a.qr_sh = p.q_rope_stride_head;
   static_assert(kBlockM == kPlanTile, "work-list tiles are the forward's query tiles");
-  const int cap = plan_capacity(p.total_tokens, p.numseqs, p.max_seqlen_all);
-  int2* plan = (int2*)p.workspace;
+  const int cap_items = plan_capacity(p.total_tokens, p.numseqs, p.max_seqlen_all);
+  // key-range parts when the workspace has room for their slots (small grids)
+  const FwdWorkspace full = fwd_workspace_layout(cap_items, p.num_q_heads, D, true);
+  const bool chunks = full.chunk_slots > 0 && p.workspace_bytes >= full.total;
+  const FwdWorkspace ws = chunks ? full : fwd_workspace_layout(cap_items, p.num_q_heads, D, false);
+  const int cap = ws.list_cap;
+  int4* plan = (int4*)((char*)p.workspace + ws.list);
   a.plan = plan;
   a.cap = cap;
-  a.kscan = (const int*)((char*)p.workspace + fwd_kscan_offset(cap));
+  a.kscan = (const int*)((char*)p.workspace + ws.kscan);
+  a.chunk_ctr = chunks ? (int*)((char*)p.workspace + ws.ctr) : nullptr;
+  a.chunk_part = chunks ? (char*)p.workspace + ws.part : nullptr;
   if (cap > 0) {
-    pro.plan[pro.nplan++] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
-                                      p.total_tokens, /*kind=*/0, a.group, cap, plan);
+    pro.plan[pro.nplan] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
+                                    p.total_tokens, /*kind=*/2, a.group, cap, plan);
+    if (chunks) {
+      pro.plan[pro.nplan].split_heads = p.num_q_heads;
+      pro.plan[pro.nplan].slots = kFwdChunkWgs;
+      pro.plan[pro.nplan].max_pairs = ws.chunk_slots;
+      pro.plan[pro.nplan].zero = a.chunk_ctr;
+      pro.plan[pro.nplan].n_zero = ws.chunk_slots * p.num_q_heads;
+    }
+    ++pro.nplan;
     if (p.split_mode == MIMIR_SPLIT_AUTO) {  // the K scan behind the split decision
       pro.kscan = kscan_args(a.k, a.k_st, a.k_sh, a.T, p.num_kv_heads, D, p.softmax_scale, (int*)a.kscan);
       pro.has_kscan = 1;

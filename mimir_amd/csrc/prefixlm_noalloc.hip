@@ -2,10 +2,12 @@
 // for callers that cannot allocate device memory (code under HIP graph capture,
 // tight serving loops, harnesses that forbid hipMalloc).
 //
-// The forward's only scratch memory is the heaviest-first query-tile work list
-// (int2 per 128-row tile, ceil(T / 128) + numseqs entries), which the prologue
-// writes completely on every call (entries past the last tile are padding), so
-// nothing in it has to start at zero.  Here it lives in a file-scope device array
+// The forward's only scratch memory here is the heaviest-first query-tile work
+// list (int4 per 128-row tile, ceil(T / 128) + numseqs entries) and the K scan's
+// slots, which the prologue writes completely on every call (entries past the
+// last tile are padding), so nothing in it has to start at zero.  The array is
+// far below the size at which the forward cuts key ranges into parts
+// (mimir_prefixlm_fwd_workspace_size), so those parts' slots are never used.  Here it lives in a file-scope device array
 // of kNoAllocScratchBytes, one copy per GPU, held until the process ends.  Host
 // code never passes the array's name to a kernel (in host code that name is a
 // host-side stand-in, not a device address): the device address comes from
@@ -20,7 +22,7 @@
 
 namespace {
 
-constexpr size_t kNoAllocScratchBytes = 128 * 1024;  // 16384 list entries
+constexpr size_t kNoAllocScratchBytes = 128 * 1024;  // 8064 list entries + the K-scan slots
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
@@ -62,7 +64,7 @@ extern "C" int mimir_prefixlm_fwd_noalloc(const MimirPrefixLMFwdParams* p, void*
   if (need > kNoAllocScratchBytes)
     return mimir::fail_with(MIMIR_ERR_UNSUPPORTED_SHAPE,
                             "mimir_prefixlm_fwd_noalloc: the tile work list needs " + std::to_string(need) +
-                                " bytes (ceil(total_tokens / 128) + numseqs entries of 8 bytes), above its fixed " +
+                                " bytes (ceil(total_tokens / 128) + numseqs entries of 16 bytes and 2 KiB of K-scan slots), above its fixed " +
                                 std::to_string(kNoAllocScratchBytes) +
                                 "-byte device array; use mimir_prefixlm_fwd with a workspace");
   MimirPrefixLMFwdParams q = *p;

@@ -80,7 +80,7 @@ __device__ int block_exclusive_scan(int v, int* wave_sums, int& total) {
 // Cost of tile t in 64-row steps of the consumer's loop (for kind 1 exactly
 // its iteration count G * query tiles).
 __device__ __forceinline__ int item_cost(int p, int nq, int kind, int group, int t) {
-  if (kind == 0) {
+  if (kind != 1) {
     const int kend = max(p, min(t * kPlanTile + kPlanTile, nq));
     return (kend + 63) / 64;
   }
@@ -97,6 +97,7 @@ struct PlanSmem {
   int wave_sums[kWaves];
   double wave_dsums[kWaves];
   int cut, pairs;
+  int chunk_items;  // items of the last chunk of sequences walked
 };
 
 __device__ __forceinline__ void put_item(const PlanArgs& a, int pos, int s, int t, int part, int pair) {
@@ -107,31 +108,46 @@ __device__ __forceinline__ void put_item(const PlanArgs& a, int pos, int s, int 
     ((int4*)a.items)[pos] = make_int4(s, t, part, pair);
 }
 
+// Parts of a kind-2 item of cost c at part cost `target` (0: no chunking).
+__device__ __forceinline__ int chunk_parts(int c, double target) {
+  if (target <= 0.0 || (double)c <= target) return 1;
+  const double n = ceil((double)c / target);
+  return n < (double)kFwdChunkMax ? (int)n : kFwdChunkMax;
+}
+
 // Visits every (sequence, tile) item, 256 sequences at a time: a scan of the
 // tile counts gives each sequence its first item, then the items are dealt to
 // the threads one each, so a single long sequence is spread over the workgroup
 // too.  Items costing `cut` or more count as two halves.  Without kScatter the
 // visit adds each item (or half) to its cost bucket; with kScatter it takes the
-// next position of that bucket and writes the entry.  Returns this thread's
-// share of the total cost.
+// next position of that bucket and writes the entry.  Kind 2 with `target` > 0
+// cuts items into chunk_parts(cost, target) parts instead.  With `reuse` (only
+// for numseqs <= kThreads, after a walk of the same list) the sequences' first
+// items and geometry are still in `sm` and are not loaded again.  Returns this
+// thread's share of the total cost.
 template <bool kScatter>
-__device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut) {
+__device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut, double target = 0.0, bool reuse = false) {
   double cost_sum = 0.0;
   for (int base = 0; base < a.numseqs; base += kThreads) {
-    const int s = base + (int)threadIdx.x;
-    int nt = 0, p = 0, nq = 0;
-    if (s < a.numseqs) {
-      const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
-      nt = ((a.kind == 0 ? g.nq : g.n) + kPlanTile - 1) / kPlanTile;
-      p = g.p;
-      nq = g.nq;
-    }
     int total;
-    const int first = block_exclusive_scan(nt, sm.wave_sums, total);
-    sm.first_item[threadIdx.x] = first;
-    sm.p[threadIdx.x] = p;
-    sm.nq[threadIdx.x] = nq;
-    __syncthreads();
+    if (reuse) {
+      total = sm.chunk_items;
+    } else {
+      const int s = base + (int)threadIdx.x;
+      int nt = 0, p = 0, nq = 0;
+      if (s < a.numseqs) {
+        const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+        nt = ((a.kind != 1 ? g.nq : g.n) + kPlanTile - 1) / kPlanTile;
+        p = g.p;
+        nq = g.nq;
+      }
+      const int first = block_exclusive_scan(nt, sm.wave_sums, total);
+      sm.first_item[threadIdx.x] = first;
+      sm.p[threadIdx.x] = p;
+      sm.nq[threadIdx.x] = nq;
+      if (threadIdx.x == 0) sm.chunk_items = total;
+      __syncthreads();
+    }
     for (int i = threadIdx.x; i < total; i += kThreads) {
       // the last sequence of the chunk whose first item is <= i owns item i
       int j = 0;
@@ -141,7 +157,23 @@ __device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut) {
       const int t = i - sm.first_item[j];
       const int c = item_cost(sm.p[j], sm.nq[j], a.kind, a.group, t);
       cost_sum += (double)c;
-      if (c >= cut) {
+      const int parts = a.kind == 2 ? chunk_parts(c, target) : 1;
+      if (parts > 1) {
+        const int cp = (c + parts - 1) / parts;
+        if constexpr (kScatter) {  // the parts take consecutive positions and slots
+          const int slot = atomicAdd(&sm.pairs, parts);
+          const int pos = atomicAdd(&sm.hist[bucket_of(cp)], parts);
+          for (int q = 0; q < parts; ++q) put_item(a, pos + q, base + j, t, q | (parts << 16), slot + q);
+        } else {
+          atomicAdd(&sm.hist[bucket_of(cp)], parts);
+        }
+      } else if (a.kind == 2) {
+        if constexpr (kScatter) {
+          put_item(a, atomicAdd(&sm.hist[bucket_of(c)], 1), base + j, t, 1 << 16, -1);
+        } else {
+          atomicAdd(&sm.hist[bucket_of(c)], 1);
+        }
+      } else if (c >= cut) {
         const int c1 = c / 2, c2 = c - c1;
         if constexpr (kScatter) {
           const int pair = atomicAdd(&sm.pairs, 1);
@@ -201,8 +233,40 @@ __device__ double block_sum(double v, PlanSmem& sm) {
   return total;
 }
 
+// The forward's list (kind 2): counted once; if the grid is small (fewer
+// workgroups than a.slots resident at once) the items costing more than the
+// per-workgroup average of one round are cut into parts (chunk_parts), the
+// counts are redone with the parts, and the list is written.  The parts of all
+// items number at most 2 * a.slots / a.split_heads <= a.max_pairs (each part
+// of a cut item costs more than half the target), so the chunk slots suffice.
+__device__ void plan_block_chunks(const PlanArgs& a, PlanSmem& sm) {
+  for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
+  if (threadIdx.x == 0) sm.pairs = 0;
+  for (int i = threadIdx.x; i < a.n_zero; i += kThreads) a.zero[i] = 0;
+  __syncthreads();
+  const double mine = walk_items<false>(a, sm, 0x7fffffff);
+  const bool reuse = a.numseqs <= kThreads;  // one chunk of sequences: still in sm
+  const double cost = block_sum(mine, sm);
+  int total = bucket_starts(sm, 0.0, 0);
+  double target = 0.0;
+  if (a.max_pairs > 0 && a.split_heads > 0 && (int64_t)total * a.split_heads < (int64_t)a.slots) {
+    target = cost * a.split_heads / a.slots;
+    if (target < (double)kFwdChunkMinCost) target = (double)kFwdChunkMinCost;
+    for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
+    __syncthreads();
+    walk_items<false>(a, sm, 0x7fffffff, target, reuse);
+    total = bucket_starts(sm, 0.0, 0);
+  }
+  walk_items<true>(a, sm, 0x7fffffff, target, reuse);
+  for (int i = total + threadIdx.x; i < a.cap; i += kThreads) put_item(a, i, -1, -1, 0, -1);
+}
+
 __device__ void plan_block(const PlanArgs& a) {
   __shared__ PlanSmem sm;
+  if (a.kind == 2) {
+    plan_block_chunks(a, sm);
+    return;
+  }
   const bool split = a.kind == 1 && a.split_heads > 0 && a.max_pairs > 0 && a.slots > 0;
   for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
   if (threadIdx.x == 0) {
@@ -220,10 +284,10 @@ __device__ void plan_block(const PlanArgs& a) {
   if (cut != 0x7fffffff) {  // recount with the heavy items halved
     for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
     __syncthreads();
-    walk_items<false>(a, sm, cut);
+    walk_items<false>(a, sm, cut, 0.0, a.numseqs <= kThreads);
     total = bucket_starts(sm, 0.0, 0);
   }
-  walk_items<true>(a, sm, cut);
+  walk_items<true>(a, sm, cut, 0.0, a.numseqs <= kThreads);
   for (int i = total + threadIdx.x; i < a.cap; i += kThreads) put_item(a, i, -1, -1, 0, -1);
 }
 

@@ -95,6 +95,24 @@ def set_dscore_workspace_limit(nbytes: int) -> None:
     _dscore_limit_bytes = int(nbytes)
 
 
+_fwd_key_chunks = os.environ.get("MIMIR_PREFIXLM_FWD_KEY_CHUNKS", "1") != "0"
+
+
+def set_fwd_key_chunks(enabled: bool) -> None:
+    """Whether the bf16 forward may cut the key ranges of its heaviest query tiles.
+
+    On a small grid (fewer than 512 query-tile x q-head workgroups, e.g. two
+    heads over 24k tokens) the heaviest tiles otherwise run alone at the end;
+    with this on, the forward's workspace is sized by
+    ``mimir_prefixlm_fwd_workspace_size`` (a few tens of MB on such grids) and
+    the kernel splits those tiles' key ranges into parts that are merged in a
+    fixed order, so results stay deterministic.  They differ from the uncut
+    forward only by fp32 summation order.  Default on.
+    """
+    global _fwd_key_chunks
+    _fwd_key_chunks = bool(enabled)
+
+
 _SPLIT_MODES = {"auto": _capi.SPLIT_AUTO, "always": _capi.SPLIT_ALWAYS, "never": _capi.SPLIT_NEVER}
 _split_mode = _SPLIT_MODES[os.environ.get("MIMIR_PREFIXLM_SPLIT", "auto")]
 
@@ -250,16 +268,19 @@ def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_
     q, k, v = _kernel_layout(q), _kernel_layout(k), _kernel_layout(v)
     out = torch.empty((T, hq, d), dtype=q.dtype, device=device)
     lse = torch.empty((hq, T), dtype=torch.float32, device=device)
-    ws_bytes = int(_capi.load().mimir_prefixlm_fwd_workspace_bytes(T, n, max_all))
-    ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
     p = _capi.FwdParams(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
         pl.data_ptr(), cl.data_ptr(), cu.data_ptr(),
         q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
         out.stride(0), out.stride(1), lse.stride(0),
         T, hq, hkv, d, n, _scalar(total_seqlen), max_all, int(bool(is_causal)),
-        _DTYPES[q.dtype], float(softmax_scale), ws.data_ptr(), ws_bytes,
+        _DTYPES[q.dtype], float(softmax_scale), 0, 0,
     )
+    lib = _capi.load()
+    ws_bytes = int(lib.mimir_prefixlm_fwd_workspace_size(ctypes.byref(p)) if _fwd_key_chunks
+                   else lib.mimir_prefixlm_fwd_workspace_bytes(T, n, max_all))
+    ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
     p.split_mode = _split_mode if split_mode is None else int(split_mode)
     keep = (q, k, v, pl, cl, cu, ws)
     if split_flag is not None and split_flag.numel() > 0:

@@ -49,11 +49,44 @@ def test_abi_version(lib):
     assert lib.mimir_prefixlm_abi_version() == _capi.ABI_VERSION
 
 
+def _align256(x):
+    return (x + 255) // 256 * 256
+
+
 def _fwd_workspace(T, numseqs):
-    """Forward workspace: the tile list, one int32 pair per entry, ceil(T / 128) + numseqs entries
+    """Forward workspace: the tile list, one int4 per entry, ceil(T / 128) + numseqs entries
     (max_seqlen_all unused), then 256-byte aligned the 512 int32 K-scan slots."""
     cap = -(-T // 128) + numseqs
-    return (cap * 8 + 255) // 256 * 256 + 512 * 4
+    return _align256(cap * 16) + 512 * 4
+
+
+def _fwd_workspace_chunked(T, numseqs, hq, d):
+    """With key-range parts: 1024 // hq chunk slots more list entries, then 256-byte aligned
+    the K-scan slots, one int32 arrival counter per (slot, q head), and per (slot, q head)
+    the partial O (fp32, d x 128) plus running max and sum of 64 lanes x 4 waves."""
+    slots = 1024 // hq
+    cap = -(-T // 128) + numseqs + slots
+    ctr = _align256(_align256(cap * 16) + 512 * 4)
+    part = _align256(ctr + slots * hq * 4)
+    return part + slots * hq * (4 * d * 128 + 4 * 64 * 8)
+
+
+@pytest.mark.parametrize("T,ns,hq,d,dtype,chunked", [
+    (24576, 11, 2, 128, _capi.DTYPE_BFLOAT16, True),     # 192 tiles x 2 heads < 512
+    (24576, 11, 2, 64, _capi.DTYPE_BFLOAT16, True),
+    (255 * 128, 3, 2, 128, _capi.DTYPE_BFLOAT16, True),  # 255 x 2 = 510
+    (256 * 128, 3, 2, 128, _capi.DTYPE_BFLOAT16, False),  # 256 x 2 = 512: the grid cannot be small
+    (16384, 8, 16, 128, _capi.DTYPE_BFLOAT16, False),
+    (24576, 11, 2, 128, _capi.DTYPE_FLOAT32, False),
+    (0, 0, 2, 128, _capi.DTYPE_BFLOAT16, False),
+])
+def test_fwd_workspace_size(lib, T, ns, hq, d, dtype, chunked):
+    p = _capi.FwdParams()
+    p.total_tokens, p.numseqs, p.max_seqlen_all, p.num_q_heads, p.head_dim, p.dtype = T, ns, 4096, hq, d, dtype
+    got = lib.mimir_prefixlm_fwd_workspace_size(ctypes.byref(p))
+    base = lib.mimir_prefixlm_fwd_workspace_bytes(T, ns, 4096)
+    assert got == (_fwd_workspace_chunked(T, ns, hq, d) if chunked else base), (got, base)
+    assert lib.mimir_prefixlm_fwd_workspace_size(None) == 0
 
 
 def test_workspace_bytes(lib):

@@ -1,0 +1,153 @@
+"""GPU checks of the forward's key-range parts on small grids.
+
+When fewer than 512 (query tile, q head) workgroups make up the forward's grid
+(few heads over a short packed row, e.g. the 2-head 24k-token workload), the
+work list cuts the key ranges of its heaviest query tiles into parts; each part
+runs as its own workgroup and writes its unnormalized O with its running max
+and sum, and the last part of a tile to arrive merges all parts in part order
+and writes O and lse.  The merged result differs from the uncut forward only by
+fp32 summation order, so:
+
+* against the oracle the usual bf16 bar holds (O <= 2e-2, lse <= 1e-2);
+* against the uncut forward: O within one bf16 rounding step (<= 1e-2 here,
+  |O| < 1), lse <= 1e-4, the RoPE-rotated q bitwise (the parts do not touch it);
+* two chunked runs agree bitwise (the merge order is fixed);
+* the work list really holds cut tiles (entries with parts > 1), so each case
+  exercises the merge.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+from mimir_amd import _capi, prefixlm_attn_fwd
+from mimir_amd import prefixlm as P
+from mimir_amd.workloads import make_case, make_config
+from oracle.prefixlm_oracle import chunked_forward_backward, dense_forward, dense_lse
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # (seq_lens, prefixes, hq, hkv, d, is_causal)
+    ([4000, 1500, 300], [3000, 0, 150], 2, 2, 128, False),
+    ([3000, 700], [100, 700], 2, 1, 64, False),
+    ([2500, 900, 1], [0, 400, 1], 4, 2, 128, True),
+    ([6000], [0], 8, 8, 128, False),
+]
+
+
+@pytest.fixture
+def key_chunks():
+    saved = P._fwd_key_chunks
+    yield
+    P._fwd_key_chunks = saved
+
+
+def forward(c, chunks, **kw):
+    """One forward launch through the C ABI; returns (outputs dict, cut tiles in the work list)."""
+    P._fwd_key_chunks = chunks
+    lib = _capi.load()
+    d = c.q.shape[2]
+    p, out, lse, keep = P.prepare_fwd(c.q, c.k, c.v, c.is_causal, c.prefix_lens, c.causal_lens, c.cu_seqlens,
+                                      c.total_seqlen, c.numseqs, c.max_seqlen_all, d ** -0.5, **kw)
+    _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    ws = keep[6]
+    entries = -(-c.T // 128) + int(c.numseqs)
+    if p.workspace_bytes > lib.mimir_prefixlm_fwd_workspace_bytes(c.T, int(c.numseqs), int(c.max_seqlen_all)):
+        entries += 1024 // c.q.shape[1]  # the chunk slots' list entries
+    lst = ws.view(torch.int32)[: 4 * entries].view(-1, 4).cpu()
+    cut = int(((lst[:, 0] >= 0) & ((lst[:, 2] >> 16) > 1)).sum())
+    res = {"o": out.clone(), "lse": lse.clone()}
+    for name, t in kw.items():
+        if isinstance(t, torch.Tensor) and t.dtype == c.q.dtype:
+            res[name] = t.clone()
+    return res, cut
+
+
+def close(a, b):
+    fin = torch.isfinite(b)
+    assert torch.equal(fin, torch.isfinite(a))
+    return (a[fin].double() - b[fin].double()).abs().max().item() if fin.any() else 0.0
+
+
+@pytest.mark.parametrize("idx", range(len(CASES)))
+def test_chunked_forward(device, idx, key_chunks):
+    seq_lens, prefixes, hq, hkv, d, causal = CASES[idx]
+    case = make_case(seq_lens, prefixes, hq, hkv, d, seed=40 + idx, dtype=torch.bfloat16, is_causal=causal)
+    c = case.to(device)
+    got, cut = forward(c, True)
+    again, _ = forward(c, True)
+    plain, none = forward(c, False)
+    print(f"[chunks] case {idx}: {cut} cut list entries; uncut run {none}", flush=True)
+    assert cut > 0 and none == 0
+    for key in got:
+        assert torch.equal(got[key], again[key]), key
+    assert close(got["o"], plain["o"]) <= 1e-2
+    assert close(got["lse"], plain["lse"]) <= 1e-4
+    qf, kf, vf = (t.float() for t in (case.q, case.k, case.v))
+    args = case.oracle_args()
+    o_ref = dense_forward(qf, kf, vf, case.is_causal, *args)
+    lse_ref = dense_lse(qf, kf, case.is_causal, *args)
+    errs = (close(got["o"].float().cpu(), o_ref), close(got["lse"].float().cpu(), lse_ref))
+    print(f"[chunks] case {idx}: O {errs[0]:.3g} lse {errs[1]:.3g} against the oracle", flush=True)
+    assert errs[0] <= 2e-2 and errs[1] <= 1e-2
+
+
+@pytest.mark.parametrize("split", [_capi.SPLIT_ALWAYS, _capi.SPLIT_NEVER], ids=["split", "plain"])
+def test_chunked_forward_gate_rope(device, split, key_chunks):
+    """Gated output, RoPE of q in the kernel (with the rotated q written out) and the P hi + lo
+    split all ride on the merged accumulator: chunked and uncut agree as above."""
+    case = make_case([3500, 800], [2000, 0], 2, 2, 128, seed=47, dtype=torch.bfloat16)
+    c = case.to(device)
+    T, hq, d = c.q.shape
+    g = torch.Generator().manual_seed(48)
+    pos = torch.arange(T, dtype=torch.float64)[:, None]
+    freq = 10000.0 ** (-torch.arange(0, d // 2, dtype=torch.float64) / (d // 2))
+    ang = torch.cat([pos * freq, pos * freq], dim=1)
+    rope = (ang.cos().float().to(device), ang.sin().float().to(device))
+    gate = torch.randn(T, hq, d, generator=g).to(device=device, dtype=torch.bfloat16)
+    runs = []
+    for chunks in (True, False):
+        kw = dict(gate=gate, gated_out=torch.empty_like(c.q), out_lo=torch.empty_like(c.q), split_mode=split,
+                  rope=rope, q_rope=torch.empty_like(c.q))
+        runs.append(forward(c, chunks, **kw))
+    (got, cut), (plain, _) = runs
+    assert cut > 0
+    assert torch.equal(got["q_rope"], plain["q_rope"])
+    assert close(got["o"], plain["o"]) <= 1e-2
+    assert close(got["gated_out"], plain["gated_out"]) <= 1e-2
+    assert close(got["lse"], plain["lse"]) <= 1e-4
+    if split == _capi.SPLIT_ALWAYS:  # O's low half: O - round(O), one rounding step of O at most
+        assert close(got["out_lo"].float() + got["o"].float(), plain["out_lo"].float() + plain["o"].float()) <= 1e-4
+
+
+def test_small_grid_workload_full_fp64(device, key_chunks):
+    """The 2-head 24576-token workload (11 documents) with its key ranges cut: O and lse in
+    full against the oracle's closed form in float64 (evaluated on the GPU), and the
+    backward's gradients against those of the uncut forward."""
+    case = make_config(6, seed=0)
+    c = case.to(device)
+    d = c.q.shape[2]
+    res = {}
+    for chunks in (True, False):
+        P._fwd_key_chunks = chunks
+        q, k, v = (t.clone().requires_grad_(True) for t in (c.q, c.k, c.v))
+        out, lse = prefixlm_attn_fwd(q, k, v, c.is_causal, c.prefix_lens, c.causal_lens, c.cu_seqlens,
+                                       c.total_seqlen, c.numseqs, c.max_seqlen_all)
+        out.backward(c.dout)
+        torch.cuda.synchronize()
+        res[chunks] = (out.detach(), lse, q.grad, k.grad, v.grad)
+    _, cut = forward(c, True)
+    assert cut > 0
+    c64 = [t.to(device=device, dtype=torch.float64) for t in (case.q, case.k, case.v, case.dout)]
+    o_r, lse_r, *_ = chunked_forward_backward(*c64, case.is_causal, *case.oracle_args(), chunk=2048)
+    e_o, e_l = close(res[True][0], o_r), close(res[True][1], lse_r)
+    print(f"[chunks] 24576 x 2 heads: O {e_o:.3g} lse {e_l:.3g} against fp64", flush=True)
+    assert e_o <= 2e-2 and e_l <= 1e-2
+    for i, name in ((2, "dq"), (3, "dk"), (4, "dv")):
+        e = close(res[True][i], res[False][i])
+        print(f"[chunks] 24576 x 2 heads: {name} chunked vs uncut {e:.3g}", flush=True)
+        assert e <= 5e-2, name
+    assert d == 128

@@ -344,7 +344,19 @@ def test_understated_max_seqlen_all(device):
         P._validate_metadata = saved
 
 
-def test_workspace_oom_falls_back_to_recompute(device, monkeypatch):
+@pytest.fixture
+def fwd_min_workspace():
+    """The forward with its minimum workspace (no key-range parts), so that the only large
+    float32 allocations of a step are the backward's."""
+    from mimir_amd import prefixlm as P
+
+    saved = P._fwd_key_chunks
+    P.set_fwd_key_chunks(False)
+    yield
+    P.set_fwd_key_chunks(saved)
+
+
+def test_workspace_oom_falls_back_to_recompute(device, monkeypatch, fwd_min_workspace):
     """If the backward workspace with the score-gradient region cannot be allocated, the
     backward runs with the small workspace and the recomputing dQ: same dK / dV bit for
     bit, dQ within the bar."""
@@ -377,7 +389,7 @@ def test_workspace_oom_falls_back_to_recompute(device, monkeypatch):
     check(case, device, label="after OOM fallback")
 
 
-def test_dscore_region_bounded_by_free_memory(device, monkeypatch):
+def test_dscore_region_bounded_by_free_memory(device, monkeypatch, fwd_min_workspace):
     """A large score-gradient region is requested only while it fits half of the free device
     memory: with the free memory reported just below twice the region the backward allocates
     the small workspace and recomputes dQ (dK / dV bit for bit, dQ within the bar); just above

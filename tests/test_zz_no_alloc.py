@@ -1,8 +1,10 @@
 """mimir_prefixlm_fwd_noalloc: the forward with its work list in the library's fixed
 device array instead of a caller workspace, checked through the C ABI against
-mimir_prefixlm_fwd on the same inputs (bitwise: the same kernels run), on two
-calls in a row, the second with a smaller input, and the refusal of a call whose
-work list does not fit the array.  Collected last (the file name) so that a
+mimir_prefixlm_fwd on the same inputs (bitwise: the same kernels run over the same
+work list; the array is far too small for the slots of the key-range parts, so the
+workspace forward runs with a workspace that leaves them out too), on two calls in
+a row, the second with a smaller input, and the refusal of a call whose work list
+does not fit the array.  Collected last (the file name) so that a
 failure here cannot hide the other GPU tests of a -x run."""
 
 import ctypes
@@ -16,7 +18,8 @@ from mimir_amd.workloads import make_case
 
 pytestmark = pytest.mark.gpu
 
-SCRATCH_BYTES = 128 * 1024  # the array's stated size: 16384 list entries of 8 bytes
+SCRATCH_BYTES = 128 * 1024  # the array's stated size: 8064 list entries of 16 bytes + 2 KiB K-scan slots
+MAX_ENTRIES = (SCRATCH_BYTES - 2048) // 16
 
 
 def _lib():
@@ -28,8 +31,14 @@ def _forward(case, device, noalloc):
     lib = _lib()
     scale = 1.0 / case.q.shape[2] ** 0.5
     out_lo = torch.empty_like(c.q)
-    p, out, lse, keep = P.prepare_fwd(c.q, c.k, c.v, case.is_causal, c.prefix_lens, c.causal_lens, c.cu_seqlens,
-                                      c.total_seqlen, c.numseqs, c.max_seqlen_all, scale, out_lo=out_lo)
+    saved = P._fwd_key_chunks
+    P.set_fwd_key_chunks(False)  # the minimum workspace: no key-range parts
+    try:
+        p, out, lse, keep = P.prepare_fwd(c.q, c.k, c.v, case.is_causal, c.prefix_lens, c.causal_lens,
+                                          c.cu_seqlens, c.total_seqlen, c.numseqs, c.max_seqlen_all, scale,
+                                          out_lo=out_lo)
+    finally:
+        P._fwd_key_chunks = saved
     stream = torch.cuda.current_stream(device).cuda_stream
     if noalloc:
         p.workspace, p.workspace_bytes = None, 0  # the entry point brings its own
@@ -55,7 +64,9 @@ def test_noalloc_forward_matches_workspace_forward(device):
 def test_noalloc_refuses_a_work_list_beyond_its_array(device):
     lib = _lib()
     p = _capi.FwdParams()
-    p.total_tokens, p.numseqs, p.max_seqlen_all = 128 * (SCRATCH_BYTES // 8), 1, 4096  # 16385 entries
+    # the largest list that fits fills the array exactly
+    assert lib.mimir_prefixlm_fwd_workspace_bytes(128 * (MAX_ENTRIES - 1), 1, 4096) == SCRATCH_BYTES
+    p.total_tokens, p.numseqs, p.max_seqlen_all = 128 * MAX_ENTRIES, 1, 4096  # one entry more
     rc = lib.mimir_prefixlm_fwd_noalloc(ctypes.byref(p), None)
     assert rc == _capi.ERR_UNSUPPORTED_SHAPE
     assert b"131072-byte device array" in lib.mimir_prefixlm_last_error()
