@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MIMIR_PREFIXLM_ABI_VERSION 7
+#define MIMIR_PREFIXLM_ABI_VERSION 8
 
 /* Element types of q/k/v/out/dout/dq/dk/dv (lse and the workspace are float32). */
 enum MimirDType {
@@ -213,6 +213,16 @@ typedef struct MimirPrefixLMBwdParams {
   const float* rope_cos;
   const float* rope_sin;
   int64_t rope_stride_token;
+  /* Key-range parts of the DQ stage (bf16; no reference counterpart): non-zero
+   * lets mimir_prefixlm_bwd_workspace_size include, where the grid can be small
+   * (ceil(total_tokens / 128) * num_q_heads < 512), a copy of the dQ tile list
+   * with room for parts, arrival counters and 1024 / num_q_heads partial slots
+   * of (4 * head_dim * 128 + 2048) bytes per q head; with a workspace that
+   * large the dQ kernels cut the key ranges of their heaviest query tiles into
+   * up to 16 parts run as separate workgroups, and the last part of a tile to
+   * arrive sums the parts in part order (deterministic) and stores dQ.  0: no
+   * parts. */
+  int32_t dq_key_chunks;
 } MimirPrefixLMBwdParams;
 
 /* Bytes of device workspace the forward needs: the heaviest-first tile work list
@@ -290,8 +300,10 @@ size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_he
 
 /* Bytes of backward workspace for these parameters: mimir_prefixlm_bwd_workspace_bytes
  * plus, with a gate, the attention's upstream gradient [T, Hq, D] in the element type,
- * plus the score-gradient tiles when mimir_prefixlm_bwd_dscore_bytes(params) is non-zero.
- * Only the size fields, head_dim, dtype, gate and dscore_limit_bytes are read. */
+ * plus the score-gradient tiles when mimir_prefixlm_bwd_dscore_bytes(params) is non-zero,
+ * plus the DQ stage's key-range parts when dq_key_chunks asks for them and the grid can
+ * be small.  Only the size fields, head_dim, dtype, gate, dscore_limit_bytes and
+ * dq_key_chunks are read. */
 size_t mimir_prefixlm_bwd_workspace_size(const MimirPrefixLMBwdParams* params);
 
 /* Bytes of workspace the score-gradient hand-off takes for these parameters, 0

@@ -16,7 +16,7 @@ from pathlib import Path
 
 # MIMIR_PREFIXLM_LIB overrides the in-tree library (e.g. to A/B two builds).
 LIB_PATH = Path(os.environ.get("MIMIR_PREFIXLM_LIB") or Path(__file__).resolve().parent / "_lib" / "libmimir_prefixlm.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_FLOAT32 = 0
 DTYPE_BFLOAT16 = 1
@@ -82,6 +82,7 @@ class BwdParams(ctypes.Structure):
         ("out_lo", _vp), ("out_lo_stride_token", _i64), ("out_lo_stride_head", _i64),
         ("split_mode", _i32), ("split_flag", _vp),
         ("rope_cos", _vp), ("rope_sin", _vp), ("rope_stride_token", _i64),
+        ("dq_key_chunks", _i32),
     ]
 
 

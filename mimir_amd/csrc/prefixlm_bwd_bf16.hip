@@ -46,7 +46,8 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   const bool gated = p.gate != nullptr;
   const size_t ds_bytes = mimir_prefixlm_bwd_dscore_bytes(&p);
   const BwdWorkspace ws = bwd_workspace_layout(p.total_tokens, p.num_q_heads, p.numseqs, p.max_seqlen_all,
-                                               gated ? (size_t)p.total_tokens * p.num_q_heads * D * 2 : 0, ds_bytes);
+                                               gated ? (size_t)p.total_tokens * p.num_q_heads * D * 2 : 0, ds_bytes,
+                                               bwd_chunk_head_dim(p));
   char* const wsb = (char*)p.workspace;
   const DscoreGeom dsg = dscore_geometry(p.total_tokens, p.num_q_heads, p.numseqs, p.max_seqlen_all);
   a.dscore = ds_bytes > 0 ? (bf16_t*)(wsb + ws.dscore) : nullptr;
@@ -54,9 +55,12 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   a.ds_width = dsg.width;
   a.delta = (float*)(wsb + ws.delta);
   a.lse2 = (float*)(wsb + ws.lse2);
-  a.plan_q = (int2*)(wsb + ws.plan_q);
+  // with key-range chunks the dQ list lives in the chunk section, with room for the parts
+  a.plan_q = (int4*)(wsb + (ws.chunk_slots > 0 ? ws.chunk_list : ws.plan_q));
   a.plan_k = (int4*)(wsb + ws.plan_k);
-  a.cap_q = ws.cap_q;
+  a.cap_q = ws.cap_q + ws.chunk_slots;
+  a.chunk_ctr = ws.chunk_slots > 0 ? (int*)(wsb + ws.chunk_ctr) : nullptr;
+  a.chunk_part = ws.chunk_slots > 0 ? wsb + ws.chunk_part : nullptr;
   a.cap_k = ws.cap_k;
   a.plan = a.plan_q;
   a.split_ctr = (int*)(wsb + ws.counters);
@@ -119,8 +123,16 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
     pk.zero = a.split_ctr;  // split counters, the dK / dV work queue and the dS-incomplete flag
     pk.n_zero = ws.pair_heads + kCounterWordsAfterPairs;
     pro.plan[pro.nplan++] = pk;
-    pro.plan[pro.nplan++] = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal,
-                                      p.total_tokens, /*kind=*/0, a.group, a.cap_q, a.plan_q);
+    PlanArgs pq = plan_args(p.cu_seqlens, p.prefix_lens, p.numseqs, p.total_seqlen, p.is_causal, p.total_tokens,
+                            /*kind=*/2, a.group, a.cap_q, a.plan_q);
+    if (ws.chunk_slots > 0) {  // key-range parts on small grids
+      pq.split_heads = a.Hq;
+      pq.slots = kChunkWgs;
+      pq.max_pairs = ws.chunk_slots;
+      pq.zero = a.chunk_ctr;
+      pq.n_zero = ws.chunk_slots * a.Hq;
+    }
+    pro.plan[pro.nplan++] = pq;
     if (p.split_mode == MIMIR_SPLIT_AUTO && p.split_flag == nullptr) {  // no recorded decision: scan K
       pro.kscan = kscan_args(a.k, a.k_st, a.k_sh, a.T, a.Hkv, D, p.softmax_scale, (int*)(wsb + ws.kscan));
       pro.has_kscan = 1;

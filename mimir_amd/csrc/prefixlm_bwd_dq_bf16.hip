@@ -35,10 +35,11 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   const int hi = lane >> 5;
   const int rank = blockIdx.x / a.Hq;
   const int h = blockIdx.x - rank * a.Hq;
-  const int2 item = a.plan[rank];
+  const int4 item = a.plan[rank];
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int qtile = item.y;
+  const int part = item.z & 0xffff, parts = item.z >> 16;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = qtile * kBlockQ;
   if (m0 >= g.nq) return;
@@ -49,7 +50,10 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   if (a.dq_companion && !dq_needs_recompute(a, split)) return;
 
   const int wg_kend = max(g.p, min(m0 + kBlockQ, g.nq));
-  const int nkt = (wg_kend + kBlockK - 1) / kBlockK;
+  const int nkt_all = (wg_kend + kBlockK - 1) / kBlockK;
+  // key tiles [kt0, nkt) of this part (the whole range unless the list cut it)
+  const int kt0 = (int)((int64_t)part * nkt_all / parts);
+  const int nkt = (int)((int64_t)(part + 1) * nkt_all / parts);
   const int qa = m0 + wave * 32;
   const bool wave_active = qa < g.nq;
   const int w_kend_max = wave_active ? max(g.p, min(qa + 32, g.nq)) : 0;
@@ -65,9 +69,9 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   const TileLoader<D, kWaves> ldk(a.k_st, wave, lane), ldv(a.v_st, wave, lane);
 
   // Tile copies walk the key tiles in order with running addresses (adds only).
-  const bf16_t* i_k = kseq;
-  const bf16_t* i_v = vseq;
-  int i_rows = g.n;
+  const bf16_t* i_k = kseq + (int64_t)kt0 * kBlockK * a.k_st;
+  const bf16_t* i_v = vseq + (int64_t)kt0 * kBlockK * a.v_st;
+  int i_rows = g.n - kt0 * kBlockK;
   auto issue_next = [&](bf16_t* tk, bf16_t* tv) {
     ldk.issue_at(i_k, rows_bytes32(i_rows, (uint32_t)a.k_st, D), tk);
     ldv.issue_at(i_v, rows_bytes32(i_rows, (uint32_t)a.v_st, D), tv);
@@ -75,7 +79,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
     i_v += kBlockK * a.v_st;
     i_rows -= kBlockK;
   };
-  issue_next(sK0, sV0);
+  if (kt0 < nkt) issue_next(sK0, sV0);
 
   bf16x8 qf[KS], dof[KS];
 #pragma unroll
@@ -171,7 +175,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
       dq_mfmas(BoolTag<false>{});
   };
 
-  for (int kt = 0; kt < nkt; kt += 2) {
+  for (int kt = kt0; kt < nkt; kt += 2) {
     wait_vmem();
     __syncthreads();
     if (kt + 1 < nkt) issue_next(sK1, sV1);
@@ -182,6 +186,9 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
     if (kt + 2 < nkt) issue_next(sK0, sV0);
     compute(kt + 1, sK1, sV1);
   }
+
+  // A part of a cut key range: the last part of the tile to arrive sums them.
+  if (__builtin_expect(parts > 1, 0) && !dq_merge_parts<DT>(a, item, h, wave, lane, dqacc)) return;
 
   // Epilogue: each wave stages its 32 dQ rows in LDS (one K / V stage object
   // per wave, free once every wave is past the tile loop) and stores whole

@@ -49,10 +49,11 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
   const int hi = lane >> 5;
   const int rank = blockIdx.x / a.Hq;
   const int h = blockIdx.x - rank * a.Hq;
-  const int2 item = a.plan[rank];
+  const int4 item = a.plan[rank];
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int qtile = item.y;
+  const int part = item.z & 0xffff, parts = item.z >> 16;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = qtile * kBlockQ;
   if (m0 >= g.nq) return;
@@ -62,7 +63,10 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
   if (dq_needs_recompute(a, split_on(a, lane))) return;
 
   const int wg_kend = max(g.p, min(m0 + kBlockQ, g.nq));
-  const int nkt = (wg_kend + kBlockK - 1) / kBlockK;
+  const int nkt_all = (wg_kend + kBlockK - 1) / kBlockK;
+  // key tiles [kt0, nkt) of this part (the whole range unless the list cut it)
+  const int kt0 = (int)((int64_t)part * nkt_all / parts);
+  const int nkt = (int)((int64_t)(part + 1) * nkt_all / parts);
   const int qa = m0 + wave * 32;
   const bool wave_active = qa < g.nq;
   const int w_kend_max = wave_active ? max(g.p, min(qa + 32, g.nq)) : 0;
@@ -78,9 +82,9 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
       row_ok ? (uint32_t)a.ds_width * kDsBlockElems * 2 : 0u);
   const uint32_t s_voff = (uint32_t)lane * 16;
 
-  const bf16_t* i_k = kseq;
-  int i_rows = g.n;
-  int i_kt = 0;
+  const bf16_t* i_k = kseq + (int64_t)kt0 * kBlockK * a.k_st;
+  int i_rows = g.n - kt0 * kBlockK;
+  int i_kt = kt0;
   auto issue_k = [&](bf16_t* tk) {
     ldk.issue_at(i_k, rows_bytes32(i_rows, (uint32_t)a.k_st, D), tk);
     i_k += kBlockK * a.k_st;
@@ -103,8 +107,10 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
               (uint32_t)(2 * i_kt + mt) * (kDsBlockElems * 2) + c * 1024, 0, kNonTemporal);
     ++i_kt;
   };
-  issue_k(sK0);
-  issue_ds();
+  if (kt0 < nkt) {
+    issue_k(sK0);
+    issue_ds();
+  }
 
   f32x16 dqacc[DT];
 #pragma unroll
@@ -142,7 +148,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     issue_ds();
   };
-  for (int kt = 0; kt < nkt; kt += 2) {
+  for (int kt = kt0; kt < nkt; kt += 2) {
     wait_vmem();
     __syncthreads();
     if (kt + 1 < nkt) issue_k(sK1);
@@ -155,6 +161,9 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
     compute(kt + 1, sK1);
     next_ds(kt + 1);
   }
+
+  // A part of a cut key range: the last part of the tile to arrive sums them.
+  if (__builtin_expect(parts > 1, 0) && !dq_merge_parts<DT>(a, item, h, wave, lane, dqacc)) return;
 
   // Epilogue: the wave stages its 32 dQ rows in LDS (half of a K stage object,
   // free once every wave is past the tile loop), in query order, and stores

@@ -139,10 +139,10 @@ size_t mimir_prefixlm_fwd_workspace_size(const MimirPrefixLMFwdParams* p) {
   if (p == nullptr) return 0;
   const size_t base = mimir_prefixlm_fwd_workspace_bytes(p->total_tokens, p->numseqs, p->max_seqlen_all);
   // key-range parts: bf16 only, and only where the grid can be small (a list of
-  // at least ceil(T / 128) query tiles per q head fills kFwdChunkWgs otherwise)
-  if (base == 0 || p->dtype != MIMIR_DTYPE_BFLOAT16 || p->num_q_heads <= 0 || p->head_dim <= 0) return base;
-  const int64_t tiles = ((int64_t)p->total_tokens + mimir::kPlanTile - 1) / mimir::kPlanTile;
-  if (tiles * p->num_q_heads >= mimir::kFwdChunkWgs) return base;
+  // at least ceil(T / 128) query tiles per q head fills kChunkWgs otherwise)
+  if (base == 0 || p->dtype != MIMIR_DTYPE_BFLOAT16 || p->head_dim <= 0 ||
+      !mimir::chunk_grid_can_be_small(p->total_tokens, p->num_q_heads))
+    return base;
   const int cap = mimir::plan_capacity(p->total_tokens, p->numseqs, p->max_seqlen_all);
   return mimir::fwd_workspace_layout(cap, p->num_q_heads, p->head_dim, true).total;
 }
@@ -163,7 +163,7 @@ size_t mimir_prefixlm_bwd_workspace_size(const MimirPrefixLMBwdParams* p) {
                                                      (size_t)elem_bytes_of(p->dtype)
                                                : 0;
   return mimir::bwd_workspace_layout(p->total_tokens, p->num_q_heads, p->numseqs, p->max_seqlen_all, dout_bytes,
-                                     mimir_prefixlm_bwd_dscore_bytes(p))
+                                     mimir_prefixlm_bwd_dscore_bytes(p), mimir::bwd_chunk_head_dim(*p))
       .total;
 }
 

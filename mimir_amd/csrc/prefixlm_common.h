@@ -447,8 +447,8 @@ struct PlanArgs {
   // kind 2 (the forward's query tiles, int4 (sequence, tile, part | parts << 16,
   // chunk slot)): when the grid is small (items * split_heads < slots) the key
   // range of every item costing more than (total cost * split_heads / slots,
-  // at least kFwdChunkMinCost) is cut into parts of about that cost, at most
-  // kFwdChunkMax; max_pairs (the chunk slots available) = 0 disables it.
+  // at least kChunkMinCost) is cut into parts of about that cost, at most
+  // kChunkMax; max_pairs (the chunk slots available) = 0 disables it.
   // kind 1: split items costing more than (total cost * split_heads / slots) / 2,
   // heaviest first and whole cost buckets at a time, up to max_pairs items;
   // split_heads = 0 disables splitting.
@@ -475,19 +475,26 @@ constexpr int kSplitSlotFloats = 2 * 128 * 128;   // dK + dV partial of one part
 // max_seqlen_all), so that the recomputing dQ kernel takes over from the hand-off.
 constexpr int kKScanSlots = 512;
 
-// Key-range chunks of the forward (kind-2 list): small grids leave most CUs idle
-// while the heaviest query tiles run, so their key ranges are cut into parts
-// that run as separate workgroups and are merged by the last to finish.
-constexpr int kFwdChunkMax = 16;        // parts per query tile
-constexpr int kFwdChunkMinCost = 4;     // key tiles per part, at least
-constexpr int kFwdChunkWgs = 512;       // forward workgroups resident at once (2 per CU)
-constexpr int kFwdChunkHeadSlots = 2 * kFwdChunkWgs;  // chunk slots x q heads, at most
+// Key-range chunks of the query-tile lists (kind 2: the forward and dQ): small
+// grids leave most CUs idle while the heaviest query tiles run, so their key
+// ranges are cut into parts that run as separate workgroups and are merged by
+// the last to finish.
+constexpr int kChunkMax = 16;        // parts per query tile
+constexpr int kChunkMinCost = 4;     // key tiles per part, at least
+constexpr int kChunkWgs = 512;       // query-tile workgroups resident at once (2 per CU)
+constexpr int kChunkHeadSlots = 2 * kChunkWgs;  // chunk slots x q heads, at most
 // Chunk slots for Hq heads: with parts cut at the per-workgroup average cost
-// of one round, the parts of the split tiles number at most 2 * kFwdChunkWgs / Hq.
-inline int fwd_chunk_slots(int hq) { return hq > 0 ? kFwdChunkHeadSlots / hq : 0; }
-// One chunk slot per (part, q head): the part's unnormalized O (fp32, per wave
-// DT * 4 float4 per lane, lane-major) then its running max and sum per lane.
-__host__ __device__ inline size_t fwd_chunk_slot_bytes(int d) { return (size_t)4 * (size_t)d * 128 + (size_t)4 * 64 * 8; }
+// of one round, the parts of the split tiles number at most 2 * kChunkWgs / Hq.
+inline int chunk_slots(int hq) { return hq > 0 ? kChunkHeadSlots / hq : 0; }
+// One chunk slot per (part, q head): the part's fp32 accumulator (O^T or dQ^T;
+// per wave DT * 4 float4 per lane, lane-major) then, for the forward, its
+// running max and sum per lane.
+__host__ __device__ inline size_t chunk_slot_bytes(int d) { return (size_t)4 * (size_t)d * 128 + (size_t)4 * 64 * 8; }
+// The grid of a kind-2 list can be small (chunks may be planned) only if the
+// ceil(T / 128) query tiles a packing has at least, times Hq, stay below kChunkWgs.
+inline bool chunk_grid_can_be_small(int total_tokens, int hq) {
+  return total_tokens > 0 && hq > 0 && ((int64_t)total_tokens + 127) / 128 * hq < kChunkWgs;
+}
 // Forward workspace, 256-byte aligned sections: the work list (int4 [cap +
 // chunk slots]), the kKScanSlots int32 slots of the K scan, then with chunking
 // one arrival counter per (chunk slot, q head) and the chunk slots.
@@ -498,13 +505,13 @@ struct FwdWorkspace {
 inline FwdWorkspace fwd_workspace_layout(int cap, int hq, int d, bool chunks) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   FwdWorkspace w;
-  w.chunk_slots = chunks && cap > 0 ? fwd_chunk_slots(hq) : 0;
+  w.chunk_slots = chunks && cap > 0 ? chunk_slots(hq) : 0;
   w.list_cap = cap > 0 ? cap + w.chunk_slots : 0;
   w.list = 0;
   w.kscan = align((size_t)w.list_cap * 16);
   w.ctr = align(w.kscan + (size_t)kKScanSlots * sizeof(int));
   w.part = align(w.ctr + (size_t)w.chunk_slots * (size_t)(hq > 0 ? hq : 0) * sizeof(int));
-  w.total = w.chunk_slots > 0 ? w.part + (size_t)w.chunk_slots * (size_t)hq * fwd_chunk_slot_bytes(d)
+  w.total = w.chunk_slots > 0 ? w.part + (size_t)w.chunk_slots * (size_t)hq * chunk_slot_bytes(d)
                               : w.ctr;
   return w;
 }
@@ -513,12 +520,22 @@ constexpr int kCounterWordsAfterPairs = 3;  // work queue next / finished, dS-in
 
 // Backward workspace sections (byte offsets, 256-byte aligned).
 // `dout_bytes`: the gated backward's upstream-gradient buffer (0 without a gate).
+// Backward workspace; with chunk_head_dim > 0 it ends with the dQ list's
+// key-range chunks: that list (int4 [cap_q + chunk slots]), one arrival counter
+// per (chunk slot, q head) and the chunk slots (chunk_slot_bytes(head_dim)).
 struct BwdWorkspace {
-  size_t delta, lse2, plan_q, plan_k, counters, kscan, slots, dout, dscore, total;
-  int cap_q, cap_k, pair_heads;
+  size_t delta, lse2, plan_q, plan_k, counters, kscan, slots, dout, dscore, chunk_list, chunk_ctr, chunk_part, total;
+  int cap_q, cap_k, pair_heads, chunk_slots;
 };
 BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all,
-                                  size_t dout_bytes = 0, size_t dscore_bytes = 0);
+                                  size_t dout_bytes = 0, size_t dscore_bytes = 0, int chunk_head_dim = 0);
+// head_dim of the dQ list's key-range chunks for these parameters, 0: none.
+inline int bwd_chunk_head_dim(const MimirPrefixLMBwdParams& p) {
+  return p.dq_key_chunks != 0 && p.dtype == MIMIR_DTYPE_BFLOAT16 && p.head_dim > 0 &&
+                 chunk_grid_can_be_small(p.total_tokens, p.num_q_heads)
+             ? p.head_dim
+             : 0;
+}
 
 // Score-gradient hand-off from the dK / dV stage to the dQ stage: bf16 dS in
 // blocks of 32 queries x 32 keys (2 KiB), block index (h * rows + row) * width +

@@ -57,7 +57,7 @@ struct FwdArgs {
   int split_mode;      // MimirSplitMode: P as bf16 hi + lo in O^T += V^T P^T
   int* split_flag;     // optional: the decision, for the backward
   int* chunk_ctr;      // arrival counter per (first chunk slot of a tile, q head)
-  char* chunk_part;    // partials per (chunk slot, q head), fwd_chunk_slot_bytes(D) each
+  char* chunk_part;    // partials per (chunk slot, q head), chunk_slot_bytes(D) each
   RopeTab rope;        // optional RoPE of Q, applied to the loaded fragments
   bf16_t* q_rope;      // optional: the rotated Q rows, for the backward
   int64_t qr_st, qr_sh;
@@ -336,7 +336,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
     constexpr int kDevScope = 16;  // buffer cache policy: coherent at device scope
     constexpr uint32_t kOBytes = (uint32_t)D * 128 * 4;
     const int slot0 = item.w - part;
-    const size_t slot_bytes = fwd_chunk_slot_bytes(D);
+    const size_t slot_bytes = chunk_slot_bytes(D);
     char* const mine = a.chunk_part + ((size_t)item.w * a.Hq + h) * slot_bytes;
     {
       const __amdgpu_buffer_rsrc_t r = make_rsrc(mine, (uint32_t)slot_bytes);
@@ -557,7 +557,7 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t str
                                     p.total_tokens, /*kind=*/2, a.group, cap, plan);
     if (chunks) {
       pro.plan[pro.nplan].split_heads = p.num_q_heads;
-      pro.plan[pro.nplan].slots = kFwdChunkWgs;
+      pro.plan[pro.nplan].slots = kChunkWgs;
       pro.plan[pro.nplan].max_pairs = ws.chunk_slots;
       pro.plan[pro.nplan].zero = a.chunk_ctr;
       pro.plan[pro.nplan].n_zero = ws.chunk_slots * p.num_q_heads;

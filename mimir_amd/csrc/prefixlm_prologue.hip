@@ -112,7 +112,7 @@ __device__ __forceinline__ void put_item(const PlanArgs& a, int pos, int s, int 
 __device__ __forceinline__ int chunk_parts(int c, double target) {
   if (target <= 0.0 || (double)c <= target) return 1;
   const double n = ceil((double)c / target);
-  return n < (double)kFwdChunkMax ? (int)n : kFwdChunkMax;
+  return n < (double)kChunkMax ? (int)n : kChunkMax;
 }
 
 // Visits every (sequence, tile) item, 256 sequences at a time: a scan of the
@@ -251,7 +251,7 @@ __device__ void plan_block_chunks(const PlanArgs& a, PlanSmem& sm) {
   double target = 0.0;
   if (a.max_pairs > 0 && a.split_heads > 0 && (int64_t)total * a.split_heads < (int64_t)a.slots) {
     target = cost * a.split_heads / a.slots;
-    if (target < (double)kFwdChunkMinCost) target = (double)kFwdChunkMinCost;
+    if (target < (double)kChunkMinCost) target = (double)kChunkMinCost;
     for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
     __syncthreads();
     walk_items<false>(a, sm, 0x7fffffff, target, reuse);
@@ -480,7 +480,7 @@ PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int nu
 }
 
 BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs, int max_seqlen_all,
-                                  size_t dout_bytes, size_t dscore_bytes) {
+                                  size_t dout_bytes, size_t dscore_bytes, int chunk_head_dim) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   BwdWorkspace w;
   const size_t rows = (size_t)(total_tokens > 0 ? total_tokens : 0) * (size_t)(num_q_heads > 0 ? num_q_heads : 0);
@@ -491,7 +491,7 @@ BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs
   w.delta = 0;
   w.lse2 = align(w.delta + rows * sizeof(float));
   w.plan_q = align(w.lse2 + rows * sizeof(float));
-  w.plan_k = align(w.plan_q + (size_t)w.cap_q * sizeof(int2));
+  w.plan_k = align(w.plan_q + (size_t)w.cap_q * sizeof(int4));
   w.counters = align(w.plan_k + (size_t)w.cap_k * sizeof(int4));
   w.kscan = align(w.counters + ((size_t)w.pair_heads + kCounterWordsAfterPairs) * sizeof(int));
   w.slots = align(w.kscan + (size_t)kKScanSlots * sizeof(int));
@@ -499,6 +499,12 @@ BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs
   w.total = dout_bytes > 0 ? w.dout + dout_bytes : w.slots + (size_t)w.pair_heads * 2 * kSplitSlotFloats * sizeof(float);
   w.dscore = align(w.total);
   if (dscore_bytes > 0) w.total = w.dscore + dscore_bytes;
+  w.chunk_slots = chunk_head_dim > 0 && w.cap_q > 0 ? chunk_slots(num_q_heads) : 0;
+  w.chunk_list = align(w.total);
+  w.chunk_ctr = align(w.chunk_list + (size_t)(w.cap_q + w.chunk_slots) * sizeof(int4));
+  w.chunk_part = align(w.chunk_ctr + (size_t)w.chunk_slots * (size_t)(num_q_heads > 0 ? num_q_heads : 0) * sizeof(int));
+  if (w.chunk_slots > 0)
+    w.total = w.chunk_part + (size_t)w.chunk_slots * (size_t)num_q_heads * chunk_slot_bytes(chunk_head_dim);
   return w;
 }
 

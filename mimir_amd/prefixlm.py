@@ -95,22 +95,23 @@ def set_dscore_workspace_limit(nbytes: int) -> None:
     _dscore_limit_bytes = int(nbytes)
 
 
-_fwd_key_chunks = os.environ.get("MIMIR_PREFIXLM_FWD_KEY_CHUNKS", "1") != "0"
+_key_chunks = os.environ.get("MIMIR_PREFIXLM_KEY_CHUNKS", "1") != "0"
 
 
-def set_fwd_key_chunks(enabled: bool) -> None:
-    """Whether the bf16 forward may cut the key ranges of its heaviest query tiles.
+def set_key_chunks(enabled: bool) -> None:
+    """Whether the bf16 forward and dQ kernels may cut the key ranges of their heaviest query tiles.
 
     On a small grid (fewer than 512 query-tile x q-head workgroups, e.g. two
     heads over 24k tokens) the heaviest tiles otherwise run alone at the end;
     with this on, the forward's workspace is sized by
-    ``mimir_prefixlm_fwd_workspace_size`` (a few tens of MB on such grids) and
-    the kernel splits those tiles' key ranges into parts that are merged in a
-    fixed order, so results stay deterministic.  They differ from the uncut
-    forward only by fp32 summation order.  Default on.
+    ``mimir_prefixlm_fwd_workspace_size`` and the backward's asks for the dQ
+    parts (``dq_key_chunks``; a few tens of MB each on such grids), and the
+    kernels split those tiles' key ranges into parts that are merged in a fixed
+    order, so results stay deterministic.  They differ from the uncut kernels
+    only by fp32 summation order.  Default on.
     """
-    global _fwd_key_chunks
-    _fwd_key_chunks = bool(enabled)
+    global _key_chunks
+    _key_chunks = bool(enabled)
 
 
 _SPLIT_MODES = {"auto": _capi.SPLIT_AUTO, "always": _capi.SPLIT_ALWAYS, "never": _capi.SPLIT_NEVER}
@@ -277,7 +278,7 @@ def prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_
         _DTYPES[q.dtype], float(softmax_scale), 0, 0,
     )
     lib = _capi.load()
-    ws_bytes = int(lib.mimir_prefixlm_fwd_workspace_size(ctypes.byref(p)) if _fwd_key_chunks
+    ws_bytes = int(lib.mimir_prefixlm_fwd_workspace_size(ctypes.byref(p)) if _key_chunks
                    else lib.mimir_prefixlm_fwd_workspace_bytes(T, n, max_all))
     ws = torch.empty(max(ws_bytes // 4, 4), dtype=torch.float32, device=device)
     p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
@@ -412,6 +413,7 @@ def prepare_bwd(dout, q, k, v, out, lse, is_causal, prefix_lens, causal_lens, cu
     if rope is not None:
         gate_keep = gate_keep + _set_rope(p, rope, T, d, device)
     p.dscore_limit_bytes = _dscore_limit_bytes
+    p.dq_key_chunks = int(_key_chunks)
     region = int(lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p))) if _dscore_limit_bytes > 0 else 0
     if region > _total_device_bytes(device) // 64:  # a large region: keep it to half of what is free
         p.dscore_limit_bytes = min(_dscore_limit_bytes, _free_device_bytes(device) // 2)

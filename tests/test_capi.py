@@ -100,7 +100,7 @@ def test_workspace_bytes(lib):
 
 def _bwd_workspace(T, hq, numseqs, max_len):
     """Backward workspace: 256-byte aligned sections delta and lse*log2(e) (float32 [Hq, T]), the
-    query-tile list (int2 per tile), the key-tile list (int4 per tile plus one per possible split pair),
+    query-tile list (int4 per tile), the key-tile list (int4 per tile plus one per possible split pair),
     one int32 counter per split (pair, kv head) plus two work-queue counters and the dS-incomplete flag,
     512 int32 K-scan slots, and two float32 slots of 2 * 128 * 128 per split (pair, kv head)."""
     def align(x):
@@ -109,11 +109,40 @@ def _bwd_workspace(T, hq, numseqs, max_len):
     pair_heads = min(384, cap * hq)
     lse2 = align(T * hq * 4)
     plan_q = align(lse2 + T * hq * 4)
-    plan_k = align(plan_q + cap * 8)
+    plan_k = align(plan_q + cap * 16)
     counters = align(plan_k + (cap + pair_heads) * 16)
     kscan = align(counters + (pair_heads + 3) * 4)
     slots = align(kscan + 512 * 4)
     return slots + pair_heads * 2 * 2 * 128 * 128 * 4
+
+
+@pytest.mark.parametrize("T,ns,hq,d,dtype,chunked", [
+    (24576, 11, 2, 128, _capi.DTYPE_BFLOAT16, True),
+    (24576, 11, 2, 64, _capi.DTYPE_BFLOAT16, True),
+    (256 * 128, 3, 2, 128, _capi.DTYPE_BFLOAT16, False),  # the grid cannot be small
+    (24576, 11, 2, 128, _capi.DTYPE_FLOAT32, False),
+])
+def test_bwd_workspace_with_dq_chunks(lib, T, ns, hq, d, dtype, chunked):
+    """dq_key_chunks adds, after the rest of the workspace, the dQ list with room for the parts
+    (int4 [cap + 1024 // hq]), one int32 counter per (chunk slot, q head) and the chunk slots;
+    only where the grid can be small (ceil(T / 128) * hq < 512) and for bf16."""
+    def align(x):
+        return (x + 255) // 256 * 256
+    p = _capi.BwdParams()
+    p.total_tokens, p.num_q_heads, p.num_kv_heads, p.numseqs, p.max_seqlen_all = T, hq, hq, ns, 4096
+    p.head_dim, p.dtype = d, dtype
+    base = lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p))
+    assert base == _bwd_workspace(T, hq, ns, 4096)
+    p.dq_key_chunks = 1
+    got = lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p))
+    if not chunked:
+        assert got == base
+        return
+    slots = 1024 // hq
+    cap = -(-T // 128) + ns
+    ctr = align(align(base) + (cap + slots) * 16)
+    part = align(ctr + slots * hq * 4)
+    assert got == part + slots * hq * (4 * d * 128 + 4 * 64 * 8)
 
 
 def test_tile_list_capacity_covers_every_packing(lib):

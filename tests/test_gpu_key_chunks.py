@@ -1,4 +1,4 @@
-"""GPU checks of the forward's key-range parts on small grids.
+"""GPU checks of the key-range parts of the forward and dQ kernels on small grids.
 
 When fewer than 512 (query tile, q head) workgroups make up the forward's grid
 (few heads over a short packed row, e.g. the 2-head 24k-token workload), the
@@ -14,6 +14,11 @@ fp32 summation order, so:
 * two chunked runs agree bitwise (the merge order is fixed);
 * the work list really holds cut tiles (entries with parts > 1), so each case
   exercises the merge.
+
+The dQ kernels (from the stored score gradients, and recomputing) cut the same
+way and sum their parts in part order: with one forward's O and lse, the
+backward with and without dQ parts gives dK / dV bitwise and dQ within one bf16
+rounding step, and the cut backward matches the oracle at the bf16 bar.
 """
 
 import ctypes
@@ -24,7 +29,7 @@ import torch
 from mimir_amd import _capi, prefixlm_attn_fwd
 from mimir_amd import prefixlm as P
 from mimir_amd.workloads import make_case, make_config
-from oracle.prefixlm_oracle import chunked_forward_backward, dense_forward, dense_lse
+from oracle.prefixlm_oracle import chunked_forward_backward, dense_backward, dense_forward, dense_lse
 
 pytestmark = pytest.mark.gpu
 
@@ -39,14 +44,14 @@ CASES = [
 
 @pytest.fixture
 def key_chunks():
-    saved = P._fwd_key_chunks
+    saved = P._key_chunks
     yield
-    P._fwd_key_chunks = saved
+    P._key_chunks = saved
 
 
 def forward(c, chunks, **kw):
     """One forward launch through the C ABI; returns (outputs dict, cut tiles in the work list)."""
-    P._fwd_key_chunks = chunks
+    P._key_chunks = chunks
     lib = _capi.load()
     d = c.q.shape[2]
     p, out, lse, keep = P.prepare_fwd(c.q, c.k, c.v, c.is_causal, c.prefix_lens, c.causal_lens, c.cu_seqlens,
@@ -124,15 +129,15 @@ def test_chunked_forward_gate_rope(device, split, key_chunks):
 
 
 def test_small_grid_workload_full_fp64(device, key_chunks):
-    """The 2-head 24576-token workload (11 documents) with its key ranges cut: O and lse in
-    full against the oracle's closed form in float64 (evaluated on the GPU), and the
-    backward's gradients against those of the uncut forward."""
+    """The 2-head 24576-token workload (11 documents) with the key ranges of the forward and
+    dQ cut: O, lse, dQ, dK and dV in full against the oracle's closed form in float64
+    (evaluated on the GPU), and the gradients against those of the uncut kernels."""
     case = make_config(6, seed=0)
     c = case.to(device)
     d = c.q.shape[2]
     res = {}
     for chunks in (True, False):
-        P._fwd_key_chunks = chunks
+        P._key_chunks = chunks
         q, k, v = (t.clone().requires_grad_(True) for t in (c.q, c.k, c.v))
         out, lse = prefixlm_attn_fwd(q, k, v, c.is_causal, c.prefix_lens, c.causal_lens, c.cu_seqlens,
                                        c.total_seqlen, c.numseqs, c.max_seqlen_all)
@@ -142,12 +147,75 @@ def test_small_grid_workload_full_fp64(device, key_chunks):
     _, cut = forward(c, True)
     assert cut > 0
     c64 = [t.to(device=device, dtype=torch.float64) for t in (case.q, case.k, case.v, case.dout)]
-    o_r, lse_r, *_ = chunked_forward_backward(*c64, case.is_causal, *case.oracle_args(), chunk=2048)
+    o_r, lse_r, dq_r, dk_r, dv_r = chunked_forward_backward(*c64, case.is_causal, *case.oracle_args(), chunk=2048)
     e_o, e_l = close(res[True][0], o_r), close(res[True][1], lse_r)
-    print(f"[chunks] 24576 x 2 heads: O {e_o:.3g} lse {e_l:.3g} against fp64", flush=True)
-    assert e_o <= 2e-2 and e_l <= 1e-2
+    e_g = [close(res[True][i], r) for i, r in ((2, dq_r), (3, dk_r), (4, dv_r))]
+    print(f"[chunks] 24576 x 2 heads: O {e_o:.3g} lse {e_l:.3g} dq/dk/dv {e_g} against fp64", flush=True)
+    assert e_o <= 2e-2 and e_l <= 1e-2 and max(e_g) <= 5e-2
     for i, name in ((2, "dq"), (3, "dk"), (4, "dv")):
         e = close(res[True][i], res[False][i])
         print(f"[chunks] 24576 x 2 heads: {name} chunked vs uncut {e:.3g}", flush=True)
         assert e <= 5e-2, name
     assert d == 128
+
+
+def _align(x):
+    return (x + 255) // 256 * 256
+
+
+def backward(c, out, lse, chunks, d):
+    """One backward launch through the C ABI with the given forward outputs; returns
+    (dq, dk, dv, cut dQ list entries)."""
+    P._key_chunks = chunks
+    lib = _capi.load()
+    p, dq, dk, dv, keep = P.prepare_bwd(c.dout, c.q, c.k, c.v, out, lse, c.is_causal, c.prefix_lens, c.causal_lens,
+                                        c.cu_seqlens, c.total_seqlen, c.numseqs, c.max_seqlen_all, d ** -0.5)
+    _capi.raise_for_status(lib, lib.mimir_prefixlm_bwd(ctypes.byref(p), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    cut = 0
+    if p.dq_key_chunks:
+        saved = p.dq_key_chunks
+        p.dq_key_chunks = 0
+        base = int(lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p)))
+        p.dq_key_chunks = saved
+        if p.workspace_bytes > base:  # the dQ list with its parts sits after the rest
+            entries = -(-c.T // 128) + int(c.numseqs) + 1024 // c.q.shape[1]
+            ws = keep[9].view(torch.uint8)[_align(base): _align(base) + 16 * entries].view(torch.int32)
+            lst = ws.view(-1, 4).cpu()
+            cut = int(((lst[:, 0] >= 0) & ((lst[:, 2] >> 16) > 1)).sum())
+    return dq.clone(), dk.clone(), dv.clone(), cut
+
+
+@pytest.fixture
+def dscore_limit():
+    saved = P._dscore_limit_bytes
+    yield
+    P._dscore_limit_bytes = saved
+
+
+@pytest.mark.parametrize("handoff", [True, False], ids=["handoff", "recompute"])
+@pytest.mark.parametrize("idx", range(len(CASES)))
+def test_chunked_dq(device, idx, handoff, key_chunks, dscore_limit):
+    seq_lens, prefixes, hq, hkv, d, causal = CASES[idx]
+    case = make_case(seq_lens, prefixes, hq, hkv, d, seed=50 + idx, dtype=torch.bfloat16, is_causal=causal)
+    c = case.to(device)
+    P.set_dscore_workspace_limit((4 << 30) if handoff else 0)
+    fwd, _ = forward(c, True)
+    got = backward(c, fwd["o"], fwd["lse"], True, d)
+    again = backward(c, fwd["o"], fwd["lse"], True, d)
+    plain = backward(c, fwd["o"], fwd["lse"], False, d)
+    print(f"[chunks] dQ case {idx} ({'hand-off' if handoff else 'recompute'}): {got[3]} cut list entries", flush=True)
+    assert got[3] > 0 and plain[3] == 0
+    for a, b in zip(got[:3], again[:3]):
+        assert torch.equal(a, b)
+    assert torch.equal(got[1], plain[1]) and torch.equal(got[2], plain[2])
+    e = close(got[0], plain[0])
+    print(f"[chunks] dQ case {idx}: chunked vs uncut {e:.3g}", flush=True)
+    assert e <= 1e-2
+    qf, kf, vf, dof = (t.float() for t in (case.q, case.k, case.v, case.dout))
+    args = case.oracle_args()
+    o_ref = dense_forward(qf, kf, vf, case.is_causal, *args)
+    refs = dense_backward(qf, kf, vf, o_ref, dof, case.is_causal, *args)
+    errs = [close(g.float().cpu(), r) for g, r in zip(got[:3], refs)]
+    print(f"[chunks] dQ case {idx}: dq/dk/dv {errs} against the oracle", flush=True)
+    assert max(errs) <= 5e-2

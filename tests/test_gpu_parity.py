@@ -350,10 +350,10 @@ def fwd_min_workspace():
     float32 allocations of a step are the backward's."""
     from mimir_amd import prefixlm as P
 
-    saved = P._fwd_key_chunks
-    P.set_fwd_key_chunks(False)
+    saved = P._key_chunks
+    P.set_key_chunks(False)
     yield
-    P.set_fwd_key_chunks(saved)
+    P.set_key_chunks(saved)
 
 
 def test_workspace_oom_falls_back_to_recompute(device, monkeypatch, fwd_min_workspace):

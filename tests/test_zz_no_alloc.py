@@ -31,14 +31,14 @@ def _forward(case, device, noalloc):
     lib = _lib()
     scale = 1.0 / case.q.shape[2] ** 0.5
     out_lo = torch.empty_like(c.q)
-    saved = P._fwd_key_chunks
-    P.set_fwd_key_chunks(False)  # the minimum workspace: no key-range parts
+    saved = P._key_chunks
+    P.set_key_chunks(False)  # the minimum workspace: no key-range parts
     try:
         p, out, lse, keep = P.prepare_fwd(c.q, c.k, c.v, case.is_causal, c.prefix_lens, c.causal_lens,
                                           c.cu_seqlens, c.total_seqlen, c.numseqs, c.max_seqlen_all, scale,
                                           out_lo=out_lo)
     finally:
-        P._fwd_key_chunks = saved
+        P._key_chunks = saved
     stream = torch.cuda.current_stream(device).cuda_stream
     if noalloc:
         p.workspace, p.workspace_bytes = None, 0  # the entry point brings its own
