@@ -22,6 +22,7 @@ rounding step, and the cut backward matches the oracle at the bf16 bar.
 """
 
 import ctypes
+import math
 
 import pytest
 import torch
@@ -49,8 +50,52 @@ def key_chunks():
     P._key_chunks = saved
 
 
-def forward(c, chunks, **kw):
-    """One forward launch through the C ABI; returns (outputs dict, cut tiles in the work list)."""
+def check_plan(case, lst, hq, chunked):
+    """The query-tile list pinned against its definition: every 128-row tile of every sequence
+    appears exactly once, whole (part 0 of 1, no chunk slot) or as parts 0 .. parts - 1 with
+    consecutive chunk slots no other tile uses; a tile is cut, into ceil(cost / target) parts (at
+    most 16), exactly when the grid is small (tiles x Hq < 512) and its cost exceeds target =
+    max(total cost x Hq / 512, 4) (cost: the key tiles of 64 its rows attend); entries run heaviest
+    first by the cost of what each runs, ceil(cost / parts); padding (-1) only after the last."""
+    total = int(case.total_seqlen)
+    cu = [int(x) for x in case.cu_seqlens[: len(case.seq_lens) + 1]]
+    expect = {}
+    for s, (n, p) in enumerate(zip(case.seq_lens, case.prefixes)):
+        nq = max(0, min(n, total - cu[s]))
+        p = 0 if case.is_causal else min(p, n)
+        for t in range(-(-nq // 128)):
+            expect[(s, t)] = -(-max(p, min(128 * t + 128, nq)) // 64)
+    cost_total = sum(expect.values())
+    small = chunked and len(expect) * hq < 512
+    target = max(cost_total * hq / 512, 4.0) if small else 0.0
+    seen, costs, slots, padding = {}, [], set(), False
+    for x, y, z, w in lst.tolist():
+        if x < 0:
+            padding = True
+            continue
+        assert not padding, "an entry after the padding"
+        part, parts = z & 0xFFFF, z >> 16
+        c = expect[(x, y)]
+        want = 1 if not small or c <= target else min(math.ceil(c / target), 16)
+        assert parts == want, ((x, y), c, parts, want)
+        if parts == 1:
+            assert part == 0 and w == -1
+        else:
+            assert 0 <= part < parts and w >= 0 and w not in slots
+            slots.add(w)
+        seen.setdefault((x, y), []).append((part, w))
+        costs.append(min(-(-c // parts), 4095))
+    assert set(seen) == set(expect)
+    for key, ps in seen.items():
+        ps.sort()
+        assert [q for q, _ in ps] == list(range(len(ps)))
+        assert len({w - q for q, w in ps}) == 1  # consecutive slots
+    assert all(a >= b for a, b in zip(costs, costs[1:])), "not heaviest first"
+
+
+def forward(c, chunks, case=None, **kw):
+    """One forward launch through the C ABI; returns (outputs dict, cut tiles in the work list).
+    With `case`, the work list is checked against its definition (check_plan)."""
     P._key_chunks = chunks
     lib = _capi.load()
     d = c.q.shape[2]
@@ -64,6 +109,8 @@ def forward(c, chunks, **kw):
         entries += 1024 // c.q.shape[1]  # the chunk slots' list entries
     lst = ws.view(torch.int32)[: 4 * entries].view(-1, 4).cpu()
     cut = int(((lst[:, 0] >= 0) & ((lst[:, 2] >> 16) > 1)).sum())
+    if case is not None:
+        check_plan(case, lst, c.q.shape[1], chunks)
     res = {"o": out.clone(), "lse": lse.clone()}
     for name, t in kw.items():
         if isinstance(t, torch.Tensor) and t.dtype == c.q.dtype:
@@ -82,9 +129,9 @@ def test_chunked_forward(device, idx, key_chunks):
     seq_lens, prefixes, hq, hkv, d, causal = CASES[idx]
     case = make_case(seq_lens, prefixes, hq, hkv, d, seed=40 + idx, dtype=torch.bfloat16, is_causal=causal)
     c = case.to(device)
-    got, cut = forward(c, True)
+    got, cut = forward(c, True, case)
     again, _ = forward(c, True)
-    plain, none = forward(c, False)
+    plain, none = forward(c, False, case)
     print(f"[chunks] case {idx}: {cut} cut list entries; uncut run {none}", flush=True)
     assert cut > 0 and none == 0
     for key in got:
@@ -144,7 +191,7 @@ def test_small_grid_workload_full_fp64(device, key_chunks):
         out.backward(c.dout)
         torch.cuda.synchronize()
         res[chunks] = (out.detach(), lse, q.grad, k.grad, v.grad)
-    _, cut = forward(c, True)
+    _, cut = forward(c, True, case)
     assert cut > 0
     c64 = [t.to(device=device, dtype=torch.float64) for t in (case.q, case.k, case.v, case.dout)]
     o_r, lse_r, dq_r, dk_r, dv_r = chunked_forward_backward(*c64, case.is_causal, *case.oracle_args(), chunk=2048)
@@ -163,9 +210,9 @@ def _align(x):
     return (x + 255) // 256 * 256
 
 
-def backward(c, out, lse, chunks, d):
+def backward(c, out, lse, chunks, d, case=None):
     """One backward launch through the C ABI with the given forward outputs; returns
-    (dq, dk, dv, cut dQ list entries)."""
+    (dq, dk, dv, cut dQ list entries); with `case` the dQ list is checked (check_plan)."""
     P._key_chunks = chunks
     lib = _capi.load()
     p, dq, dk, dv, keep = P.prepare_bwd(c.dout, c.q, c.k, c.v, out, lse, c.is_causal, c.prefix_lens, c.causal_lens,
@@ -183,6 +230,8 @@ def backward(c, out, lse, chunks, d):
             ws = keep[9].view(torch.uint8)[_align(base): _align(base) + 16 * entries].view(torch.int32)
             lst = ws.view(-1, 4).cpu()
             cut = int(((lst[:, 0] >= 0) & ((lst[:, 2] >> 16) > 1)).sum())
+            if case is not None:
+                check_plan(case, lst, c.q.shape[1], True)
     return dq.clone(), dk.clone(), dv.clone(), cut
 
 
@@ -201,7 +250,7 @@ def test_chunked_dq(device, idx, handoff, key_chunks, dscore_limit):
     c = case.to(device)
     P.set_dscore_workspace_limit((4 << 30) if handoff else 0)
     fwd, _ = forward(c, True)
-    got = backward(c, fwd["o"], fwd["lse"], True, d)
+    got = backward(c, fwd["o"], fwd["lse"], True, d, case)
     again = backward(c, fwd["o"], fwd["lse"], True, d)
     plain = backward(c, fwd["o"], fwd["lse"], False, d)
     print(f"[chunks] dQ case {idx} ({'hand-off' if handoff else 'recompute'}): {got[3]} cut list entries", flush=True)
