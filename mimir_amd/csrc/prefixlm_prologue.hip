@@ -89,9 +89,15 @@ __device__ __forceinline__ int item_cost(int p, int nq, int kind, int group, int
 }
 
 __device__ __forceinline__ int bucket_of(int cost) { return min(cost, kPlanBuckets - 1); }
+// LDS slot of bucket b: one padding word every 16 buckets, so that the 16
+// consecutive buckets each thread owns in bucket_starts sit in distinct banks
+// across the wave.
+constexpr int kHistSlots = kPlanBuckets + kPlanBuckets / 16;
+__device__ __forceinline__ int bucket_slot(int b) { return b + (b >> 4); }
+__device__ __forceinline__ int hist_slot(int cost) { return bucket_slot(bucket_of(cost)); }
 
 struct PlanSmem {
-  int hist[kPlanBuckets];
+  int hist[kHistSlots];
   int first_item[kThreads];  // per sequence of the current chunk
   int p[kThreads], nq[kThreads];
   int wave_sums[kWaves];
@@ -106,6 +112,23 @@ __device__ __forceinline__ void put_item(const PlanArgs& a, int pos, int s, int 
     ((int2*)a.items)[pos] = make_int2(s, t);
   else
     ((int4*)a.items)[pos] = make_int4(s, t, part, pair);
+}
+
+// n consecutive indices from *counter for each lane of the wave (0 for none):
+// a wave-wide exclusive scan and one atomic per wave.  Every lane of the wave
+// must call it.
+__device__ __forceinline__ int wave_alloc(int* counter, int n) {
+  const int lane = threadIdx.x & 63;
+  int x = n;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  int base = 0;
+  if (lane == 63 && x > 0) base = atomicAdd(counter, x);
+  base = __shfl(base, 63, 64);
+  return base + x - n;
 }
 
 // Parts of a kind-2 item of cost c at part cost `target` (0: no chunking).
@@ -123,11 +146,14 @@ __device__ __forceinline__ int chunk_parts(int c, double target) {
 // next position of that bucket and writes the entry.  Kind 2 with `target` > 0
 // cuts items into chunk_parts(cost, target) parts instead.  With `reuse` (only
 // for numseqs <= kThreads, after a walk of the same list) the sequences' first
-// items and geometry are still in `sm` and are not loaded again.  Returns this
-// thread's share of the total cost.
+// items and geometry are still in `sm` and are not loaded again; `pre` is this
+// thread's sequence of the first chunk, loaded by the caller ahead of time.
+// Returns this thread's share of the total cost.
 template <bool kScatter>
-__device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut, double target = 0.0, bool reuse = false) {
+__device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut, double target = 0.0, bool reuse = false,
+                             const SeqGeom* pre = nullptr, int* items = nullptr) {
   double cost_sum = 0.0;
+  if (items != nullptr) *items = 0;
   for (int base = 0; base < a.numseqs; base += kThreads) {
     int total;
     if (reuse) {
@@ -136,7 +162,9 @@ __device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut, double ta
       const int s = base + (int)threadIdx.x;
       int nt = 0, p = 0, nq = 0;
       if (s < a.numseqs) {
-        const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+        const SeqGeom g = base == 0 && pre != nullptr
+                              ? *pre
+                              : load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
         nt = ((a.kind != 1 ? g.nq : g.n) + kPlanTile - 1) / kPlanTile;
         p = g.p;
         nq = g.nq;
@@ -148,45 +176,56 @@ __device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut, double ta
       if (threadIdx.x == 0) sm.chunk_items = total;
       __syncthreads();
     }
-    for (int i = threadIdx.x; i < total; i += kThreads) {
+    if (items != nullptr) *items += total;
+    // Uniform trip count (every lane runs every round), so that the chunk slots
+    // and pair indices are dealt by one atomic per wave instead of one per item.
+    for (int i0 = 0; i0 < total; i0 += kThreads) {
+      const int i = i0 + (int)threadIdx.x;
+      const bool valid = i < total;
       // the last sequence of the chunk whose first item is <= i owns item i
-      int j = 0;
+      int j = 0, t = 0, c = 0;
+      if (valid) {
 #pragma unroll
-      for (int step = kThreads / 2; step > 0; step >>= 1)
-        if (sm.first_item[j + step] <= i) j += step;
-      const int t = i - sm.first_item[j];
-      const int c = item_cost(sm.p[j], sm.nq[j], a.kind, a.group, t);
-      cost_sum += (double)c;
-      const int parts = a.kind == 2 ? chunk_parts(c, target) : 1;
+        for (int step = kThreads / 2; step > 0; step >>= 1)
+          if (sm.first_item[j + step] <= i) j += step;
+        t = i - sm.first_item[j];
+        c = item_cost(sm.p[j], sm.nq[j], a.kind, a.group, t);
+        cost_sum += (double)c;
+      }
+      const int parts = valid && a.kind == 2 ? chunk_parts(c, target) : 1;
+      int slot = 0;  // first chunk slot (kind 2 parts) or pair index (kind 1 halves)
+      if (kScatter && (a.kind == 2 ? target > 0.0 : cut != 0x7fffffff)) {  // uniform
+        const int n = !valid ? 0 : a.kind == 2 ? (parts > 1 ? parts : 0) : (a.kind == 1 && c >= cut ? 1 : 0);
+        slot = wave_alloc(&sm.pairs, n);
+      }
+      if (!valid) continue;
       if (parts > 1) {
         const int cp = (c + parts - 1) / parts;
         if constexpr (kScatter) {  // the parts take consecutive positions and slots
-          const int slot = atomicAdd(&sm.pairs, parts);
-          const int pos = atomicAdd(&sm.hist[bucket_of(cp)], parts);
+          const int pos = atomicAdd(&sm.hist[hist_slot(cp)], parts);
           for (int q = 0; q < parts; ++q) put_item(a, pos + q, base + j, t, q | (parts << 16), slot + q);
         } else {
-          atomicAdd(&sm.hist[bucket_of(cp)], parts);
+          atomicAdd(&sm.hist[hist_slot(cp)], parts);
         }
       } else if (a.kind == 2) {
         if constexpr (kScatter) {
-          put_item(a, atomicAdd(&sm.hist[bucket_of(c)], 1), base + j, t, 1 << 16, -1);
+          put_item(a, atomicAdd(&sm.hist[hist_slot(c)], 1), base + j, t, 1 << 16, -1);
         } else {
-          atomicAdd(&sm.hist[bucket_of(c)], 1);
+          atomicAdd(&sm.hist[hist_slot(c)], 1);
         }
       } else if (c >= cut) {
         const int c1 = c / 2, c2 = c - c1;
         if constexpr (kScatter) {
-          const int pair = atomicAdd(&sm.pairs, 1);
-          put_item(a, atomicAdd(&sm.hist[bucket_of(c1)], 1), base + j, t, 1, pair);
-          put_item(a, atomicAdd(&sm.hist[bucket_of(c2)], 1), base + j, t, 2, pair);
+          put_item(a, atomicAdd(&sm.hist[hist_slot(c1)], 1), base + j, t, 1, slot);
+          put_item(a, atomicAdd(&sm.hist[hist_slot(c2)], 1), base + j, t, 2, slot);
         } else {
-          atomicAdd(&sm.hist[bucket_of(c1)], 1);
-          atomicAdd(&sm.hist[bucket_of(c2)], 1);
+          atomicAdd(&sm.hist[hist_slot(c1)], 1);
+          atomicAdd(&sm.hist[hist_slot(c2)], 1);
         }
       } else if constexpr (kScatter) {
-        put_item(a, atomicAdd(&sm.hist[bucket_of(c)], 1), base + j, t, 0, -1);
+        put_item(a, atomicAdd(&sm.hist[hist_slot(c)], 1), base + j, t, 0, -1);
       } else {
-        atomicAdd(&sm.hist[bucket_of(c)], 1);
+        atomicAdd(&sm.hist[hist_slot(c)], 1);
       }
     }
     __syncthreads();  // the chunk arrays are rewritten by the next chunk
@@ -204,7 +243,7 @@ __device__ int bucket_starts(PlanSmem& sm, double threshold, int max_pairs) {
   int local = 0;
 #pragma unroll
   for (int j = 0; j < kBucketsPerThread; ++j) {
-    cnt[j] = sm.hist[kPlanBuckets - 1 - (kBucketsPerThread * threadIdx.x + j)];
+    cnt[j] = sm.hist[bucket_slot(kPlanBuckets - 1 - (kBucketsPerThread * threadIdx.x + j))];
     local += cnt[j];
   }
   int total;
@@ -213,7 +252,7 @@ __device__ int bucket_starts(PlanSmem& sm, double threshold, int max_pairs) {
 #pragma unroll
   for (int j = 0; j < kBucketsPerThread; ++j) {
     const int b = kPlanBuckets - 1 - (kBucketsPerThread * threadIdx.x + j);
-    sm.hist[b] = run;  // becomes the next free position of bucket b
+    sm.hist[bucket_slot(b)] = run;  // becomes the next free position of bucket b
     run += cnt[j];     // items of cost >= b
     if (max_pairs > 0 && (double)b > threshold && run <= max_pairs) cut = b;
   }
@@ -233,30 +272,42 @@ __device__ double block_sum(double v, PlanSmem& sm) {
   return total;
 }
 
-// The forward's list (kind 2): counted once; if the grid is small (fewer
-// workgroups than a.slots resident at once) the items costing more than the
-// per-workgroup average of one round are cut into parts (chunk_parts), the
-// counts are redone with the parts, and the list is written.  The parts of all
+// A query-tile list (kind 2: the forward's, dQ's): counted once (items and
+// cost); if the grid is small (fewer workgroups than a.slots resident at once)
+// the items costing more than the per-workgroup average of one round are cut
+// into parts (chunk_parts) and the counts are redone with the parts; then the
+// bucket positions are scanned and the list is written.  The parts of all
 // items number at most 2 * a.slots / a.split_heads <= a.max_pairs (each part
 // of a cut item costs more than half the target), so the chunk slots suffice.
+// The first chunk's sequence geometry, loaded before the zeroing so that its
+// latency overlaps it.
+__device__ __forceinline__ SeqGeom prefetch_seq(const PlanArgs& a) {
+  SeqGeom g{};
+  if ((int)threadIdx.x < a.numseqs)
+    g = load_seq(a.cu_seqlens, a.prefix_lens, threadIdx.x, a.total_seqlen, a.is_causal, a.T);
+  return g;
+}
+
 __device__ void plan_block_chunks(const PlanArgs& a, PlanSmem& sm) {
-  for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
+  const SeqGeom pre = prefetch_seq(a);
+  for (int i = threadIdx.x; i < kHistSlots; i += kThreads) sm.hist[i] = 0;
   if (threadIdx.x == 0) sm.pairs = 0;
   for (int i = threadIdx.x; i < a.n_zero; i += kThreads) a.zero[i] = 0;
   __syncthreads();
-  const double mine = walk_items<false>(a, sm, 0x7fffffff);
+  int items = 0;
+  const double mine = walk_items<false>(a, sm, 0x7fffffff, 0.0, false, &pre, &items);
   const bool reuse = a.numseqs <= kThreads;  // one chunk of sequences: still in sm
-  const double cost = block_sum(mine, sm);
-  int total = bucket_starts(sm, 0.0, 0);
+  int total;
   double target = 0.0;
-  if (a.max_pairs > 0 && a.split_heads > 0 && (int64_t)total * a.split_heads < (int64_t)a.slots) {
-    target = cost * a.split_heads / a.slots;
+  if (a.max_pairs > 0 && a.split_heads > 0 && (int64_t)items * a.split_heads < (int64_t)a.slots) {
+    // small grid: recount with the cut items' parts (the first counts are not used)
+    target = block_sum(mine, sm) * a.split_heads / a.slots;
     if (target < (double)kChunkMinCost) target = (double)kChunkMinCost;
-    for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
+    for (int i = threadIdx.x; i < kHistSlots; i += kThreads) sm.hist[i] = 0;
     __syncthreads();
     walk_items<false>(a, sm, 0x7fffffff, target, reuse);
-    total = bucket_starts(sm, 0.0, 0);
   }
+  total = bucket_starts(sm, 0.0, 0);
   walk_items<true>(a, sm, 0x7fffffff, target, reuse);
   for (int i = total + threadIdx.x; i < a.cap; i += kThreads) put_item(a, i, -1, -1, 0, -1);
 }
@@ -268,21 +319,22 @@ __device__ void plan_block(const PlanArgs& a) {
     return;
   }
   const bool split = a.kind == 1 && a.split_heads > 0 && a.max_pairs > 0 && a.slots > 0;
-  for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
+  const SeqGeom pre = prefetch_seq(a);
+  for (int i = threadIdx.x; i < kHistSlots; i += kThreads) sm.hist[i] = 0;
   if (threadIdx.x == 0) {
     sm.cut = 0x7fffffff;
     sm.pairs = 0;
   }
   for (int i = threadIdx.x; i < a.n_zero; i += kThreads) a.zero[i] = 0;
   __syncthreads();
-  const double mine = walk_items<false>(a, sm, 0x7fffffff);
+  const double mine = walk_items<false>(a, sm, 0x7fffffff, 0.0, false, &pre);
   double threshold = 0.0;
   if (split)  // half the average per compute unit
     threshold = block_sum(mine, sm) * a.split_heads / a.slots / 2.0;
   int total = bucket_starts(sm, threshold, split ? a.max_pairs : 0);
   const int cut = sm.cut;
   if (cut != 0x7fffffff) {  // recount with the heavy items halved
-    for (int i = threadIdx.x; i < kPlanBuckets; i += kThreads) sm.hist[i] = 0;
+    for (int i = threadIdx.x; i < kHistSlots; i += kThreads) sm.hist[i] = 0;
     __syncthreads();
     walk_items<false>(a, sm, cut, 0.0, a.numseqs <= kThreads);
     total = bucket_starts(sm, 0.0, 0);
