@@ -40,6 +40,7 @@ CASES = [
     ([3000, 700], [100, 700], 2, 1, 64, False),
     ([2500, 900, 1], [0, 400, 1], 4, 2, 128, True),
     ([6000], [0], 8, 8, 128, False),
+    ([2000] + [17] * 300, [1200] + [5] * 300, 1, 1, 64, False),  # > 256 sequences: the walks reload them
 ]
 
 
