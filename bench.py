@@ -467,6 +467,9 @@ def main() -> int:
             return flash_attn_varlen_prefixlm(qg, kg, vg, case.is_causal, *call_args)
 
         def run_bwd(o):
+            # q / k / v stand for the views of the projection they are in Mimir2 (layers.py:183-189):
+            # gradients flow on instead of accumulating into leaves, so no grad accumulation kernels
+            qg.grad = kg.grad = vg.grad = None
             o.backward(c.dout)
 
         def step():
