@@ -36,18 +36,25 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   constexpr int kDkKeys = DkCfg<D>::kKeys;
   using L = TileLayout<D>;
   static_assert(kBwdBlockQT == 64, "one TileLayout tile per Q / dO block");
-  __shared__ __attribute__((aligned(16))) bf16_t sQ0[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sO0[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sQ1[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sO1[L::kElems];
-  __shared__ __attribute__((aligned(16))) float sL0[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) float sD0[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) float sL1[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) float sD1[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) bf16_t sQ2[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sO2[L::kElems];
-  __shared__ __attribute__((aligned(16))) float sL2[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) float sD2[kBwdBlockQT];
+  // Three LDS stages of (Q tile, dO tile, lse2 row, delta row), each one
+  // object, so that the compiler can tell the reads of one stage from the
+  // tile copies into another (it tracks the copy targets of a few objects only).
+  constexpr int kStageElems = 2 * L::kElems + 2 * kBwdBlockQT * 2;  // Q, dO, then lse2 and delta (fp32)
+  __shared__ __attribute__((aligned(16))) bf16_t sS0[kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS1[kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS2[kStageElems];
+  bf16_t* const sQ0 = sS0;
+  bf16_t* const sO0 = sS0 + L::kElems;
+  float* const sL0 = (float*)(sS0 + 2 * L::kElems);
+  float* const sD0 = sL0 + kBwdBlockQT;
+  bf16_t* const sQ1 = sS1;
+  bf16_t* const sO1 = sS1 + L::kElems;
+  float* const sL1 = (float*)(sS1 + 2 * L::kElems);
+  float* const sD1 = sL1 + kBwdBlockQT;
+  bf16_t* const sQ2 = sS2;
+  bf16_t* const sO2 = sS2 + L::kElems;
+  float* const sL2 = (float*)(sS2 + 2 * L::kElems);
+  float* const sD2 = sL2 + kBwdBlockQT;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -93,12 +100,18 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   const bf16_t* i_o = o_head;
   const float* i_r = r_head;
   int i_qt = 0, i_rows = g.nq - q_begin;
-  auto issue_next = [&](bf16_t* tq, bf16_t* to, float* tl, float* td) {
-    ldq.issue_at(i_q, rows_bytes32(i_rows, q_st32, D), tq);
-    ldo.issue_at(i_o, rows_bytes32(i_rows, o_st32, D), to);
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(i_r, i_rows > 0 ? (uint32_t)i_rows * 4u : 0u);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(wave == 0 ? tl : td), 4,
-                                             (uint32_t)lane * 4u, 0, 0, 0);
+  // Every step issues its copies, also past the last tile (`valid` false): those
+  // copy zero bytes (their resources are empty, so no memory is read) and only
+  // write zeros to a free stage.  With the copies and the barrier waits the same
+  // on every step, the compiler can see that each stage's copies are complete
+  // before its reads (conditional copies made it wait for all copies in flight).
+  auto issue_next = [&](bool valid, bf16_t* tq, bf16_t* to, float* tl) {
+    const int rows = valid ? i_rows : 0;
+    ldq.issue_at(i_q, rows_bytes32(rows, q_st32, D), tq);
+    ldo.issue_at(i_o, rows_bytes32(rows, o_st32, D), to);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(i_r, rows > 0 ? (uint32_t)rows * 4u : 0u);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(tl + (wave == 0 ? 0 : kBwdBlockQT)),
+                                             4, (uint32_t)lane * 4u, 0, 0, 0);
     if (++i_qt == nqt) {
       i_qt = 0;
       i_rows = g.nq - q_begin;
@@ -117,7 +130,7 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   };
   // Three LDS stages: iteration it computes on stage it % 3 while the tiles of
   // it + 1 and it + 2 are in flight.
-  if (n_iter > 0) issue_next(sQ0, sO0, sL0, sD0);
+  issue_next(n_iter > 0, sQ0, sO0, sL0);
 
   bf16x8 kf[KS], vf[KS];
 #pragma unroll
@@ -126,15 +139,11 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
     kf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
     vf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rv, (uint32_t)((key * a.v_st + 16 * ks + 8 * hi) * 2)));
   }
-  if (n_iter > 1) issue_next(sQ1, sO1, sL1, sD1);
+  issue_next(n_iter > 1, sQ1, sO1, sL1);
   // Buffer loads per issue() and wave: Q and dO tiles plus one lse2 / delta row.
   constexpr int kLoadsPerIssue = 2 * TileLoader<D, kDkWaves>::kPerWave + 1;
-  auto sync_stage = [&](int it) {  // tile `it` has landed everywhere; tile it + 1 may still be in flight
-    if (it + 1 < n_iter)
-      stage_barrier<kLoadsPerIssue>();
-    else
-      stage_barrier<0>();
-  };
+  // Tile `it` has landed everywhere; the copies of tile it + 1 may still be in flight.
+  auto sync_stage = [&]() { stage_barrier<kLoadsPerIssue>(); };
 
   f32x16 dkacc[DT], dvacc[DT];
 #pragma unroll
@@ -248,18 +257,21 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
   // After the barrier of iteration it every wave is done with iteration it - 1,
   // whose stage ((it + 2) % 3) then receives tile it + 2.
   for (int it = 0; it < n_iter; it += 3) {
-    sync_stage(it);
-    if (it + 2 < n_iter) issue_next(sQ2, sO2, sL2, sD2);
+    sync_stage();
+    issue_next(it + 2 < n_iter, sQ2, sO2, sL2);
     step(sQ0, sO0, sL0, sD0);
     if (it + 1 >= n_iter) break;
-    sync_stage(it + 1);
-    if (it + 3 < n_iter) issue_next(sQ0, sO0, sL0, sD0);
+    sync_stage();
+    issue_next(it + 3 < n_iter, sQ0, sO0, sL0);
     step(sQ1, sO1, sL1, sD1);
     if (it + 2 >= n_iter) break;
-    sync_stage(it + 2);
-    if (it + 4 < n_iter) issue_next(sQ1, sO1, sL1, sD1);
+    sync_stage();
+    issue_next(it + 4 < n_iter, sQ1, sO1, sL1);
     step(sQ2, sO2, sL2, sD2);
   }
+  // The copies past the last tile (and with n_iter == 0 all loads) are still
+  // in flight: none may land in LDS after the workgroup ends.
+  wait_vmem();
 
   if (!wave_active) return;
   const int kpos = ka + l32;

@@ -38,23 +38,29 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   static_assert(kBwdBlockQT == 64, "one TileLayout tile per Q / dO block");
 
   // LDS: three stages of (Q tile, dO tile, lse2 row, delta row) and the V tile
-  // (two 64-row TileLayout tiles), each its own object so that the compiler can
-  // tell the reads of one stage from the tile copies into another.  After the
+  // (two 64-row TileLayout tiles).  Each stage is one object, so that the
+  // compiler can tell the reads of one stage from the tile copies into another
+  // (it tracks the copy targets of a few objects only: with one object per
+  // tile it made some stage's reads wait for every copy in flight).  After the
   // tile loop the Q / dO tiles of stages 0 and 1 hold the dK / dV partials of
   // the second wave of each pair.
-  __shared__ __attribute__((aligned(16))) bf16_t sQ0[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sO0[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sQ1[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sO1[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sQ2[L::kElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sO2[L::kElems];
-  __shared__ __attribute__((aligned(16))) float sL0[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) float sD0[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) float sL1[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) float sD1[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) float sL2[kBwdBlockQT];
-  __shared__ __attribute__((aligned(16))) float sD2[kBwdBlockQT];
+  constexpr int kStageElems = 2 * L::kElems + 2 * kBwdBlockQT * 2;  // Q, dO, then lse2 and delta (fp32)
+  __shared__ __attribute__((aligned(16))) bf16_t sS0[kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS1[kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS2[kStageElems];
   __shared__ __attribute__((aligned(16))) bf16_t sV[2 * L::kElems];
+  bf16_t* const sQ0 = sS0;
+  bf16_t* const sO0 = sS0 + L::kElems;
+  float* const sL0 = (float*)(sS0 + 2 * L::kElems);
+  float* const sD0 = sL0 + kBwdBlockQT;
+  bf16_t* const sQ1 = sS1;
+  bf16_t* const sO1 = sS1 + L::kElems;
+  float* const sL1 = (float*)(sS1 + 2 * L::kElems);
+  float* const sD1 = sL1 + kBwdBlockQT;
+  bf16_t* const sQ2 = sS2;
+  bf16_t* const sO2 = sS2 + L::kElems;
+  float* const sL2 = (float*)(sS2 + 2 * L::kElems);
+  float* const sD2 = sL2 + kBwdBlockQT;
   static_assert(64 * 64 * 4 <= L::kElems * 2, "one slice's partials fit one tile object");
 
   __shared__ int unit_next;  // the workgroup's next work unit
@@ -129,12 +135,18 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   const bf16_t* i_o = o_head + (int64_t)tile0 * kBwdBlockQT * a.do_st;
   const float* i_r = r_head + tile0 * kBwdBlockQT;
   int i_qt = tile0, i_rows = g.nq - q_begin - tile0 * kBwdBlockQT;
-  auto issue_next = [&](bf16_t* tq, bf16_t* to, float* tl, float* td) {
-    ldq.issue_at(i_q, rows_bytes32(i_rows, q_st32, D), tq);
-    ldo.issue_at(i_o, rows_bytes32(i_rows, o_st32, D), to);
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(i_r, i_rows > 0 ? (uint32_t)i_rows * 4u : 0u);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(wave == 0 ? tl : td), 4,
-                                             (uint32_t)lane * 4u, 0, 0, 0);
+  // Every step issues its copies, also past the last tile (`valid` false): those
+  // copy zero bytes (their resources are empty, so no memory is read) and only
+  // write zeros to a free stage.  With the copies and the barrier waits the same
+  // on every step, the compiler can see that each stage's copies are complete
+  // before its reads (conditional copies made it wait for all copies in flight).
+  auto issue_next = [&](bool valid, bf16_t* tq, bf16_t* to, float* tl) {
+    const int rows = valid ? i_rows : 0;
+    ldq.issue_at(i_q, rows_bytes32(rows, q_st32, D), tq);
+    ldo.issue_at(i_o, rows_bytes32(rows, o_st32, D), to);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(i_r, rows > 0 ? (uint32_t)rows * 4u : 0u);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(tl + (wave == 0 ? 0 : kBwdBlockQT)),
+                                             4, (uint32_t)lane * 4u, 0, 0, 0);
     if (++i_qt == nqt) {
       i_qt = 0;
       i_rows = g.nq - q_begin;
@@ -156,7 +168,7 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   // fragments of this wave's slice go to registers.
   ldv.issue(vseq, kb0, g.n, sV);
   ldv.issue(vseq, kb0 + 64, g.n, sV + L::kElems);
-  if (n_iter > 0) issue_next(sQ0, sO0, sL0, sD0);
+  issue_next(n_iter > 0, sQ0, sO0, sL0);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kseq, rows_bytes(g.n, a.k_st, D));
   bf16x8 kf[KS];
 #pragma unroll
@@ -164,14 +176,11 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     const int64_t key = ka + l32;
     kf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
   }
-  if (n_iter > 1) issue_next(sQ1, sO1, sL1, sD1);
+  issue_next(n_iter > 1, sQ1, sO1, sL1);
   constexpr int kLoadsPerIssue = 2 * Loader::kPerWave + 1;
-  auto sync_stage = [&](int it) {  // tile `it` has landed everywhere; tile it + 1 may still be in flight
-    if (it + 1 < n_iter)
-      stage_barrier<kLoadsPerIssue>();
-    else
-      stage_barrier<0>();
-  };
+  // Tile `it` has landed everywhere; the copies of tile it + 1 (and dS stores
+  // after them) may still be in flight.
+  auto sync_stage = [&]() { stage_barrier<kLoadsPerIssue>(); };
 
   f32x16 dkacc[DT], dvacc[DT];
 #pragma unroll
@@ -319,19 +328,20 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   // After the barrier of iteration it every wave is done with iteration it - 1,
   // whose stage ((it + 2) % 3) then receives tile it + 2.
   for (int it = 0; it < n_iter; it += 3) {
-    sync_stage(it);
-    if (it + 2 < n_iter) issue_next(sQ2, sO2, sL2, sD2);
+    sync_stage();
+    issue_next(it + 2 < n_iter, sQ2, sO2, sL2);
     step(sQ0, sO0, sL0, sD0);
     if (it + 1 >= n_iter) break;
-    sync_stage(it + 1);
-    if (it + 3 < n_iter) issue_next(sQ0, sO0, sL0, sD0);
+    sync_stage();
+    issue_next(it + 3 < n_iter, sQ0, sO0, sL0);
     step(sQ1, sO1, sL1, sD1);
     if (it + 2 >= n_iter) break;
-    sync_stage(it + 2);
-    if (it + 4 < n_iter) issue_next(sQ1, sO1, sL1, sD1);
+    sync_stage();
+    issue_next(it + 4 < n_iter, sQ1, sO1, sL1);
     step(sQ2, sO2, sL2, sD2);
   }
-  // With n_iter == 0 the V / K loads are still in flight here.
+  // The copies past the last tile, and with n_iter == 0 the V / K loads, are
+  // still in flight here.
   wait_vmem();
   if (tid == 0) nxt = fetch_unit();
 
