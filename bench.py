@@ -16,9 +16,13 @@ when dQ recomputes S and dP, that is not counted), so the three add up to the
 step's 14*D*Hq*N.  With the score-gradient hand-off (bf16, head_dim 128) the dQ
 kernel reads the dS blocks the dK/dV kernel stored; the line then also gives its
 streamed bytes and bandwidth (``dq_ds_bytes``, ``dq_ds_gbs``).
-Kernel durations come from a separate pass of K steps with the stages serialized
-(``mimir_prefixlm_bwd_stages``) and HIP events recorded on the launch stream
-between them; that pass and the per-step medians run before the timed region.  The CPU baseline times the oracle's restatement of the reference
+Timing: after a warm-up of at least ``--warmup`` steps and ``--warmup-seconds``
+(so the clocks settle), the timed region runs K steps back to back between two
+HIP events on the launch stream; ``value`` and ``ms_per_step`` come from it.  A
+second pass of K steps records an event at every step boundary for the per-step
+median, a third times the forward alone, and a fourth runs the stages serialized
+(``mimir_prefixlm_bwd_stages``) with events between them for the per-kernel
+durations the roofline entry uses.  The CPU baseline times the oracle's restatement of the reference
 masked-SDPA path (fp32, autograd) on a bounded sample of the same batch.
 
 Prints exactly one JSON line.
@@ -155,12 +159,32 @@ def dscore_blocks(case) -> int:
     return total
 
 
+def working_kernels(d: int, elem: int, split: bool, handoff: bool) -> dict:
+    """Full names, as rocprofv3 reports them, of the kernel instantiations that do each stage's work.
+
+    With split_mode AUTO the bf16 stages enqueue a plain and a split instantiation and
+    the one the device-side K scan does not select exits at once; ``split`` says which
+    one works.  ``handoff``: the dK/dV kernel stores dS and dq_ds_kernel reads it.
+    """
+    if elem == 4:
+        return {"fwd": f"fwd_f32_kernel<{d}>", "dkdv": f"dkdv_f32_kernel<{d}>", "dq": f"dq_f32_kernel<{d}>"}
+    flag = "true" if split else "false"
+    if d == 128:
+        dkdv = "dkdv_pair_ds_kernel" if handoff else f"dkdv_pair_kernel<{flag}>"
+    else:
+        dkdv = f"dkdv_kernel<{d}, {flag}>"
+    return {"fwd": f"fwd_bf16_kernel<{d}, {int(split)}>", "dkdv": dkdv,
+            "dq": "dq_ds_kernel" if handoff else f"dq_kernel<{d}>"}
+
+
 def _measured_traffic(workload: str, kernel: str):
-    """HBM bytes per launch of ``kernel`` on ``workload`` from the committed PMC summary.
+    """HBM bytes per launch of ``kernel`` (full instantiation name) on ``workload``.
 
     profiles/hbm_traffic.json holds FETCH_SIZE and WRITE_SIZE per dispatch from two
     rocprofv3 --pmc runs of this script, each scaled by what the same counter reads
-    for a plain 1 GiB device copy; None when the workload was not profiled.
+    for a plain 1 GiB device copy, keyed by the full instantiation name (the plain
+    and split instantiations of one kernel are separate entries); None when the
+    workload or the kernel was not profiled.
     """
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
     try:
@@ -384,6 +408,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup-seconds", type=float, default=1.0,
+                    help="warm up for at least this long (and at least --warmup steps) so that the GPU clocks settle "
+                         "before anything is timed")
     ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5, 6])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -505,31 +532,19 @@ def main() -> int:
 
     K = args.steps
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(K)]
-    for _ in range(args.warmup):
+    # Warm-up by time: at least --warmup steps and at least --warmup-seconds of them
+    # (each step synchronized, so the host clock measures GPU work), so that the
+    # clocks have settled before the timed region.
+    t_warm = time.perf_counter()
+    warm_steps = 0
+    while warm_steps < args.warmup or time.perf_counter() - t_warm < args.warmup_seconds:
         step()
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        warm_steps += 1
+    warm_s = time.perf_counter() - t_warm
 
-    # The measurement passes run first and the timed region last, so that the
-    # timed steps find the GPU clocks settled.
-    # Forward and forward + backward per step, HIP events on the launch stream: medians of K runs.
-    pe = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
-    for k in range(K):
-        pe[k][0].record()
-        o = run_fwd()
-        pe[k][1].record()
-        if not fwd_only:
-            run_bwd(o)
-        pe[k][2].record()
-    torch.cuda.synchronize()
-    fwd_med = statistics.median(e[0].elapsed_time(e[1]) for e in pe)
-    step_med = statistics.median(e[0].elapsed_time(e[2]) for e in pe)
-
-    # Per-kernel durations: K more steps with the stages serialized and bracketed by events.
-    for k in range(K):
-        staged_step(evs[k])
-    torch.cuda.synchronize()
-
-    # Timed region: K whole steps.
+    # Timed region (the `value`): K whole steps back to back, one event before the
+    # first and one after the last.
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -540,6 +555,34 @@ def main() -> int:
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
     ms_per_step = total_ms / K
+
+    # The same K steps again with an event at every step boundary: per-step
+    # durations (their median, and their mean for comparison with the timed region).
+    be = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    be[0].record()
+    for k in range(K):
+        step()
+        be[k + 1].record()
+    torch.cuda.synchronize()
+    per_step = [be[k].elapsed_time(be[k + 1]) for k in range(K)]
+    step_med = statistics.median(per_step)
+    step_evented_mean = be[0].elapsed_time(be[K]) / K
+
+    # Forward alone per step, events around it: median of K runs.
+    pe = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(K)]
+    for k in range(K):
+        pe[k][0].record()
+        o = run_fwd()
+        pe[k][1].record()
+        if not fwd_only:
+            run_bwd(o)
+    torch.cuda.synchronize()
+    fwd_med = statistics.median(e[0].elapsed_time(e[1]) for e in pe)
+
+    # Per-kernel durations: K more steps with the stages serialized and bracketed by events.
+    for k in range(K):
+        staged_step(evs[k])
+    torch.cuda.synchronize()
 
     stage_ms = {name: [evs[k][i].elapsed_time(evs[k][i + 1]) for k in range(K)] for i, (name, _) in enumerate(stages)}
     stage_avg = {name: sum(v) / len(v) for name, v in stage_ms.items()}
@@ -554,14 +597,13 @@ def main() -> int:
     peak = PEAK_F32_TFLOPS if c.q.dtype == torch.float32 else PEAK_BF16_TFLOPS
     kernel_flops = {"fwd": f_fwd, "dkdv": 8.0 * d * hq * pairs, "dq": 2.0 * d * hq * pairs}
     handoff = not fwd_only and int(lib.mimir_prefixlm_bwd_dscore_bytes(bpr)) > 0  # dQ reads dK/dV's dS
-    # the device-side AUTO rule (softmax_scale * max|K| > 0.75) on the host copy of K: with the split
-    # the recomputing dQ does the work even where the hand-off region exists
-    split = elem == 2 and not fwd_only and bool(case.k.float().abs().max().item() * scale > 0.75)
+    # the device-side AUTO rule (softmax_scale * max|K| > 0.75, over the keys inside sequences) on the
+    # host copy of K: with the split the recomputing dQ does the work even where the hand-off region exists
+    cu = case.cu_seqlens.tolist()
+    keys = case.k[cu[0]:cu[int(case.numseqs)]]
+    split = elem == 2 and keys.numel() > 0 and bool(keys.float().abs().max().item() * scale > 0.75)
     handoff = handoff and not split
-    kernel_names = {"fwd": "fwd_bf16_kernel" if elem == 2 else "fwd_f32_kernel",
-                    "dkdv": ("dkdv_pair_ds_kernel" if handoff else "dkdv_pair_kernel") if (elem == 2 and d == 128)
-                    else "dkdv_kernel",
-                    "dq": "dq_ds_kernel" if handoff else "dq_kernel"}
+    kernel_names = working_kernels(d, elem, split, handoff)
     dom = max((n for n in kernel_flops if n in stage_avg), key=lambda n: stage_avg[n])
     achieved = kernel_flops[dom] / (stage_avg[dom] * 1e-3) / 1e12
     alg_bytes = fwd_bytes(T, hq, hkv, d, elem) + (0 if fwd_only else bwd_bytes(T, hq, hkv, d, elem))
@@ -590,8 +632,17 @@ def main() -> int:
         },
         "pct_of_peak": round(100.0 * value / peak, 2),
         "hbm_gbs_algorithmic": round(alg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "timing": ("value = attended FLOPs / ms_per_step, ms_per_step = the mean of K back-to-back steps between "
+                   "two events after a time-based warm-up; step_ms_median = the median of K per-step durations from a "
+                   "second pass of K steps with an event at every step boundary (step_ms_evented_mean = that pass's "
+                   "mean)"),
+        "warmup_steps_run": warm_steps,
+        "warmup_s": round(warm_s, 3),
         "fwd_ms_median": round(fwd_med, 5),
         "step_ms_median": round(step_med, 5),
+        "step_ms_evented_mean": round(step_evented_mean, 5),
+        "step_ms_min": round(min(per_step), 5),
+        "step_ms_max": round(max(per_step), 5),
         "fwd_tflops_median": round(f_fwd / (fwd_med * 1e-3) / 1e12, 2),
         "step_tflops_median": round(flops / (step_med * 1e-3) / 1e12, 2),
         "staged_step_ms_median": round(staged_med, 5),

@@ -241,10 +241,14 @@ size_t mimir_prefixlm_fwd_workspace_bytes(int32_t total_tokens, int32_t numseqs,
  * own scheduling).  It adds 1024 / num_q_heads chunk slots of
  * (4 * head_dim * 128 + 2048) bytes per q head and their arrival counters; it
  * equals mimir_prefixlm_fwd_workspace_bytes where the grid cannot be small
- * (ceil(total_tokens / 128) * num_q_heads >= 512) and for float32.  The forward
- * cuts key ranges iff its workspace_bytes reaches this size; any size from
+ * (ceil(min(total_tokens, total_seqlen) / 128) * num_q_heads >= 512: the
+ * least number of query tiles when cu_seqlens[0] = 0, as the reference's
+ * metadata has it; with leading padding rows the grid can be smaller and then
+ * runs uncut) and for float32.  The forward cuts key ranges iff its
+ * workspace_bytes reaches this size; any size from
  * mimir_prefixlm_fwd_workspace_bytes up is valid.  Reads only dtype,
- * total_tokens, num_q_heads, head_dim, numseqs and max_seqlen_all. */
+ * total_tokens, total_seqlen, num_q_heads, head_dim, numseqs and
+ * max_seqlen_all. */
 size_t mimir_prefixlm_fwd_workspace_size(const MimirPrefixLMFwdParams* params);
 
 /* Forward: out (and lse if non-NULL).
@@ -263,7 +267,10 @@ int mimir_prefixlm_fwd(const MimirPrefixLMFwdParams* params, void* stream);
  * MIMIR_ERR_UNSUPPORTED_SHAPE before any device work (it fits while
  * ceil(total_tokens / 128) + numseqs <= 8064); it never cuts key ranges.  It calls no hipMalloc / hipFree.  Every call on one GPU
  * shares that array, so calls that overlap on one GPU (two streams or threads)
- * race; the array needs no clearing between calls.  Outputs as mimir_prefixlm_fwd. */
+ * race; the array needs no clearing between calls.  The array's device address
+ * is looked up once per device (the first call there) and kept: do not call it
+ * after a hipDeviceReset (or another re-creation of the device's primary
+ * context) in the same process.  Outputs as mimir_prefixlm_fwd. */
 int mimir_prefixlm_fwd_noalloc(const MimirPrefixLMFwdParams* params, void* stream);
 
 /* Backward: dq, dk, dv from dout, out and lse.  Deterministic: every gradient
@@ -302,8 +309,9 @@ size_t mimir_prefixlm_bwd_workspace_bytes(int32_t total_tokens, int32_t num_q_he
  * plus, with a gate, the attention's upstream gradient [T, Hq, D] in the element type,
  * plus the score-gradient tiles when mimir_prefixlm_bwd_dscore_bytes(params) is non-zero,
  * plus the DQ stage's key-range parts when dq_key_chunks asks for them and the grid can
- * be small.  Only the size fields, head_dim, dtype, gate, dscore_limit_bytes and
- * dq_key_chunks are read. */
+ * be small (the test of mimir_prefixlm_fwd_workspace_size).  Only the size fields
+ * (total_tokens, total_seqlen, num_q_heads, numseqs, max_seqlen_all), head_dim,
+ * dtype, gate, dscore_limit_bytes and dq_key_chunks are read. */
 size_t mimir_prefixlm_bwd_workspace_size(const MimirPrefixLMBwdParams* params);
 
 /* Bytes of workspace the score-gradient hand-off takes for these parameters, 0

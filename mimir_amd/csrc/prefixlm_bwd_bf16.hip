@@ -134,7 +134,8 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
     }
     pro.plan[pro.nplan++] = pq;
     if (p.split_mode == MIMIR_SPLIT_AUTO && p.split_flag == nullptr) {  // no recorded decision: scan K
-      pro.kscan = kscan_args(a.k, a.k_st, a.k_sh, a.T, a.Hkv, D, p.softmax_scale, (int*)(wsb + ws.kscan));
+      pro.kscan = kscan_args(a.k, a.k_st, a.k_sh, a.T, a.Hkv, D, p.softmax_scale, (int*)(wsb + ws.kscan),
+                             p.cu_seqlens, p.numseqs);
       pro.has_kscan = 1;
     }
   }

@@ -237,7 +237,6 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
 
     // S / dP MFMAs at raised wave priority: of the two waves on a SIMD, the one
     // ready to issue MFMAs goes first while the other runs its softmax.
-    __builtin_amdgcn_s_setprio(1);
     rd_a(0);
     rd_a(1);
 #pragma unroll
@@ -251,7 +250,6 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     rd_tr(0);
     rd_tr(1);
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_setprio(0);
     // rows of sc / dp: query qr + 8*(r/4) + 4*hi + r%4 ; column: the lane's key.
     if (masked) {
       // allowed iff qs_lane <= q < nq, i.e. (unsigned)(q - qs_lane) < (unsigned)max(nq - qs_lane, 0)

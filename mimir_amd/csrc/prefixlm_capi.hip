@@ -139,9 +139,10 @@ size_t mimir_prefixlm_fwd_workspace_size(const MimirPrefixLMFwdParams* p) {
   if (p == nullptr) return 0;
   const size_t base = mimir_prefixlm_fwd_workspace_bytes(p->total_tokens, p->numseqs, p->max_seqlen_all);
   // key-range parts: bf16 only, and only where the grid can be small (a list of
-  // at least ceil(T / 128) query tiles per q head fills kChunkWgs otherwise)
+  // at least ceil(min(T, total_seqlen) / 128) query tiles per q head fills
+  // kChunkWgs otherwise)
   if (base == 0 || p->dtype != MIMIR_DTYPE_BFLOAT16 || p->head_dim <= 0 ||
-      !mimir::chunk_grid_can_be_small(p->total_tokens, p->num_q_heads))
+      !mimir::chunk_grid_can_be_small(p->total_tokens, p->total_seqlen, p->num_q_heads))
     return base;
   const int cap = mimir::plan_capacity(p->total_tokens, p->numseqs, p->max_seqlen_all);
   return mimir::fwd_workspace_layout(cap, p->num_q_heads, p->head_dim, true).total;

@@ -490,10 +490,16 @@ inline int chunk_slots(int hq) { return hq > 0 ? kChunkHeadSlots / hq : 0; }
 // per wave DT * 4 float4 per lane, lane-major) then, for the forward, its
 // running max and sum per lane.
 __host__ __device__ inline size_t chunk_slot_bytes(int d) { return (size_t)4 * (size_t)d * 128 + (size_t)4 * 64 * 8; }
-// The grid of a kind-2 list can be small (chunks may be planned) only if the
-// ceil(T / 128) query tiles a packing has at least, times Hq, stay below kChunkWgs.
-inline bool chunk_grid_can_be_small(int total_tokens, int hq) {
-  return total_tokens > 0 && hq > 0 && ((int64_t)total_tokens + 127) / 128 * hq < kChunkWgs;
+// Whether the grid of a kind-2 list can be small (chunks may be planned), from
+// the active tokens n = min(T, total_seqlen): a packing of n tokens has at least
+// ceil(n / 128) query tiles when its sequences start at cu_seqlens[0] = 0 (the
+// reference's metadata), so the grid can be small only if that many times Hq
+// stays below kChunkWgs.  Other metadata (leading padding rows) can have fewer
+// tiles; such a call may get no chunk room and then runs uncut: slower, with
+// the same results.
+inline bool chunk_grid_can_be_small(int total_tokens, int total_seqlen, int hq) {
+  const int n = total_seqlen < total_tokens ? total_seqlen : total_tokens;
+  return n > 0 && hq > 0 && ((int64_t)n + 127) / 128 * hq < kChunkWgs;
 }
 // Forward workspace, 256-byte aligned sections: the work list (int4 [cap +
 // chunk slots]), the kKScanSlots int32 slots of the K scan, then with chunking
@@ -532,7 +538,7 @@ BwdWorkspace bwd_workspace_layout(int total_tokens, int num_q_heads, int numseqs
 // head_dim of the dQ list's key-range chunks for these parameters, 0: none.
 inline int bwd_chunk_head_dim(const MimirPrefixLMBwdParams& p) {
   return p.dq_key_chunks != 0 && p.dtype == MIMIR_DTYPE_BFLOAT16 && p.head_dim > 0 &&
-                 chunk_grid_can_be_small(p.total_tokens, p.num_q_heads)
+                 chunk_grid_can_be_small(p.total_tokens, p.total_seqlen, p.num_q_heads)
              ? p.head_dim
              : 0;
 }
@@ -599,16 +605,20 @@ struct FillArgs {
 };
 
 // K magnitude scan for the dQ split decision (see kKScanSlots): kKScanSlots
-// workgroups, each over a strided share of the [T, Hkv, D] rows.
+// workgroups, each over a strided share of the [T, Hkv, D] rows of the tokens
+// inside sequences, [cu_seqlens[0], cu_seqlens[numseqs]).
 struct KScanArgs {
   const bf16_t* k;
   int64_t k_st, k_sh;
   int T, Hkv, D;
   uint32_t thr_bits;  // bf16 magnitude bits of kSplitThreshold / softmax_scale
   int* slots;         // [kKScanSlots]
+  const int32_t* cu_seqlens;
+  int numseqs;
 };
 
-KScanArgs kscan_args(const bf16_t* k, int64_t k_st, int64_t k_sh, int T, int Hkv, int D, float scale, int* slots);
+KScanArgs kscan_args(const bf16_t* k, int64_t k_st, int64_t k_sh, int T, int Hkv, int D, float scale, int* slots,
+                     const int32_t* cu_seqlens, int numseqs);
 
 // Whether a kernel splits its bf16 operand (wave-uniform): always, never, or
 // (AUTO) as the recorded decision `flag` says, or without one when the K scan

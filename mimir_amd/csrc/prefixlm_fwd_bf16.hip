@@ -564,7 +564,8 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t str
     }
     ++pro.nplan;
     if (p.split_mode == MIMIR_SPLIT_AUTO) {  // the K scan behind the split decision
-      pro.kscan = kscan_args(a.k, a.k_st, a.k_sh, a.T, p.num_kv_heads, D, p.softmax_scale, (int*)a.kscan);
+      pro.kscan = kscan_args(a.k, a.k_st, a.k_sh, a.T, p.num_kv_heads, D, p.softmax_scale, (int*)a.kscan,
+                             p.cu_seqlens, p.numseqs);
       pro.has_kscan = 1;
     }
   }

@@ -12,9 +12,10 @@
 // code never passes the array's name to a kernel (in host code that name is a
 // host-side stand-in, not a device address): the device address comes from
 // hipGetSymbolAddress, looked up on the first call per device with that device
-// current, and only that address is used.  Every call on one GPU shares that
-// GPU's array, so calls that overlap on one GPU (two streams, two host threads)
-// race.
+// current, and kept for the life of the process (a hipDeviceReset or another
+// re-creation of the device's primary context would make it stale: the entry
+// point is not for use across one).  Every call on one GPU shares that GPU's
+// array, so calls that overlap on one GPU (two streams, two host threads) race.
 #include <mutex>
 #include <string>
 

@@ -410,14 +410,21 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
 }
 
 // K magnitude scan: workgroup b sets slot b to 1 if a bf16 element of its share
+// of the key rows inside sequences, tokens [cu_seqlens[0], cu_seqlens[numseqs])
 // of the [T, Hkv, D] rows (16-byte units b * 256 + threadIdx.x, then every
-// kKScanSlots * 256 units) has |k| > the threshold, else to 0.  Magnitudes are
-// compared as integers: for finite bf16 the bits with the sign cleared order
-// like the values (a NaN compares above any threshold and sets the slot).
+// kKScanSlots * 256 units), has |k| > the threshold, else to 0.  Padding rows
+// are never attended, so whatever they hold cannot change the decision.
+// Magnitudes are compared as integers: for finite bf16 the bits with the sign
+// cleared order like the values (a NaN compares above any threshold and sets
+// the slot).
 __device__ void kscan_block(const KScanArgs& a, int b) {
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
   const int upr = a.D / 8;  // 16-byte units per row
-  const int64_t units = (int64_t)a.T * a.Hkv * upr;
+  int first = a.numseqs > 0 ? a.cu_seqlens[0] : 0;
+  int last = a.numseqs > 0 ? a.cu_seqlens[a.numseqs] : 0;
+  first = first < 0 ? 0 : (first > a.T ? a.T : first);
+  last = last < first ? first : (last > a.T ? a.T : last);
+  const int64_t units = (int64_t)(last - first) * a.Hkv * upr;
   const int64_t step = (int64_t)kKScanSlots * kThreads;
   u16x2 mx = {0, 0};
   for (int64_t u0 = (int64_t)b * kThreads + threadIdx.x; u0 < units; u0 += 4 * step) {
@@ -429,8 +436,8 @@ __device__ void kscan_block(const KScanArgs& a, int b) {
       if (u < units) {
         const int64_t row = u / upr;
         const int c = (int)(u - row * upr);
-        const int t = (int)(row / a.Hkv), hk = (int)(row - (int64_t)t * a.Hkv);
-        w[j] = *(const i32x4*)&a.k[(int64_t)t * a.k_st + (int64_t)hk * a.k_sh + c * 8];
+        const int r = (int)(row / a.Hkv), hk = (int)(row - (int64_t)r * a.Hkv);
+        w[j] = *(const i32x4*)&a.k[(int64_t)(first + r) * a.k_st + (int64_t)hk * a.k_sh + c * 8];
       }
     }
 #pragma unroll
@@ -498,10 +505,13 @@ int plan_capacity(int total_tokens, int numseqs, int /*max_seqlen_all*/) {
   return (int)(bound < 0x7fffffff ? bound : 0x7fffffff);
 }
 
-KScanArgs kscan_args(const bf16_t* k, int64_t k_st, int64_t k_sh, int T, int Hkv, int D, float scale, int* slots) {
+KScanArgs kscan_args(const bf16_t* k, int64_t k_st, int64_t k_sh, int T, int Hkv, int D, float scale, int* slots,
+                     const int32_t* cu_seqlens, int numseqs) {
   KScanArgs ks;
   ks.k = k; ks.k_st = k_st; ks.k_sh = k_sh;
   ks.T = T; ks.Hkv = Hkv; ks.D = D;
+  ks.cu_seqlens = cu_seqlens;
+  ks.numseqs = numseqs;
   const float thr = kSplitThreshold / scale;  // as bf16 magnitude bits, rounded toward zero
   uint32_t bits;
   __builtin_memcpy(&bits, &thr, 4);

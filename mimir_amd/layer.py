@@ -128,11 +128,12 @@ class _GatedAttention(torch.autograd.Function):
         y = torch.empty((T, hq, d), dtype=gqkv.dtype, device=gqkv.device)
         # bf16: the split decision and, when the kernels split, the low half of the
         # attention output (for the backward's delta row sums)
-        out_lo = torch.empty_like(y) if bf16 else y.new_empty(0)
+        lo = P._wants_lo(y)
+        out_lo = torch.empty_like(y) if lo else y.new_empty(0)
         flag = torch.empty(1 if bf16 else 0, dtype=torch.int32, device=y.device)
         p, out, lse, keep = P.prepare_fwd(q_in if fused else q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
                                           total_seqlen, numseqs, max_seqlen_all, softmax_scale, gate=gate,
-                                          gated_out=y, out_lo=out_lo if bf16 else None, split_flag=flag,
+                                          gated_out=y, out_lo=out_lo if lo else None, split_flag=flag,
                                           rope=(cos, sin) if fused else None, q_rope=q if fused else None)
         _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), P._stream(y.device)))
         ctx.save_for_backward(gqkv, q, k, out, lse, out_lo, flag, cos, sin, prefix_lens, causal_lens, cu_seqlens)

@@ -325,7 +325,16 @@ def _gate_operand(name: str, t, shape, dtype, copy: bool = True) -> Tensor:
 
 
 def _wants_lo(q: Tensor) -> bool:
-    return q.dtype == torch.bfloat16
+    """Whether a bf16 forward keeps its output's low half for the backward.
+
+    With split mode "auto" (the default) or "always" the low half O_lo = round(O -
+    round(O)) is allocated for every bf16 call and saved for the backward: one more
+    [T, Hq, D] bf16 tensor per attention call held from forward to backward (64 MiB
+    at 8 x 2048 tokens, 16 heads, head_dim 128), written only when the kernels split.
+    "never" skips it.  The mode is read when the call is made (under torch.compile,
+    when it is traced).
+    """
+    return q.dtype == torch.bfloat16 and _split_mode != _capi.SPLIT_NEVER
 
 
 def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
@@ -335,7 +344,7 @@ def _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_se
     # backward's delta = rowsum(dO * O)); float32 needs neither
     lo = _wants_lo(q)
     out_lo = torch.empty(q.shape, dtype=q.dtype, device=q.device) if lo else q.new_empty(0)
-    flag = torch.empty(1 if lo else 0, dtype=torch.int32, device=q.device)
+    flag = torch.empty(1 if q.dtype == torch.bfloat16 else 0, dtype=torch.int32, device=q.device)
     p, out, lse, keep = prepare_fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
                                     numseqs, max_seqlen_all, softmax_scale, out_lo=out_lo if lo else None,
                                     split_flag=flag)
@@ -466,7 +475,8 @@ def _prefixlm_fwd_op(
     total_seqlen: Tensor, numseqs: Tensor, max_seqlen_all: Tensor, softmax_scale: float,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """(O, lse, O_lo, split_flag): for bf16 the low output half (written only when the
-    kernels split P) and the recorded split decision; both empty for float32."""
+    kernels split P; empty with split mode "never") and the recorded split decision;
+    both empty for float32."""
     return _fwd_impl(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
                      max_seqlen_all, softmax_scale)
 
@@ -476,7 +486,7 @@ def _(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, nu
       softmax_scale):
     cf = torch.contiguous_format
     lo = torch.empty_like(q, memory_format=cf) if _wants_lo(q) else q.new_empty(0)
-    flag = q.new_empty(1 if _wants_lo(q) else 0, dtype=torch.int32)
+    flag = q.new_empty(1 if q.dtype == torch.bfloat16 else 0, dtype=torch.int32)
     return (torch.empty_like(q, memory_format=cf), q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32), lo,
             flag)
 

@@ -71,18 +71,22 @@ def _fwd_workspace_chunked(T, numseqs, hq, d):
     return part + slots * hq * (4 * d * 128 + 4 * 64 * 8)
 
 
-@pytest.mark.parametrize("T,ns,hq,d,dtype,chunked", [
-    (24576, 11, 2, 128, _capi.DTYPE_BFLOAT16, True),     # 192 tiles x 2 heads < 512
-    (24576, 11, 2, 64, _capi.DTYPE_BFLOAT16, True),
-    (255 * 128, 3, 2, 128, _capi.DTYPE_BFLOAT16, True),  # 255 x 2 = 510
-    (256 * 128, 3, 2, 128, _capi.DTYPE_BFLOAT16, False),  # 256 x 2 = 512: the grid cannot be small
-    (16384, 8, 16, 128, _capi.DTYPE_BFLOAT16, False),
-    (24576, 11, 2, 128, _capi.DTYPE_FLOAT32, False),
-    (0, 0, 2, 128, _capi.DTYPE_BFLOAT16, False),
+@pytest.mark.parametrize("T,total,ns,hq,d,dtype,chunked", [
+    (24576, 24576, 11, 2, 128, _capi.DTYPE_BFLOAT16, True),     # 192 tiles x 2 heads < 512
+    (24576, 24576, 11, 2, 64, _capi.DTYPE_BFLOAT16, True),
+    (255 * 128, 255 * 128, 3, 2, 128, _capi.DTYPE_BFLOAT16, True),  # 255 x 2 = 510
+    (256 * 128, 256 * 128, 3, 2, 128, _capi.DTYPE_BFLOAT16, False),  # 256 x 2 = 512: cannot be small
+    (256 * 128, 3000, 3, 2, 128, _capi.DTYPE_BFLOAT16, True),  # padded: 3000 real tokens, 24 x 2 tiles
+    (256 * 128, 0, 3, 2, 128, _capi.DTYPE_BFLOAT16, False),    # no active token: nothing to cut
+    (16384, 16384, 8, 16, 128, _capi.DTYPE_BFLOAT16, False),
+    (24576, 24576, 11, 2, 128, _capi.DTYPE_FLOAT32, False),
+    (0, 0, 0, 2, 128, _capi.DTYPE_BFLOAT16, False),
 ])
-def test_fwd_workspace_size(lib, T, ns, hq, d, dtype, chunked):
+def test_fwd_workspace_size(lib, T, total, ns, hq, d, dtype, chunked):
+    """The chunk room is sized where the grid can be small: ceil(min(T, total_seqlen) / 128) x Hq < 512."""
     p = _capi.FwdParams()
     p.total_tokens, p.numseqs, p.max_seqlen_all, p.num_q_heads, p.head_dim, p.dtype = T, ns, 4096, hq, d, dtype
+    p.total_seqlen = total
     got = lib.mimir_prefixlm_fwd_workspace_size(ctypes.byref(p))
     base = lib.mimir_prefixlm_fwd_workspace_bytes(T, ns, 4096)
     assert got == (_fwd_workspace_chunked(T, ns, hq, d) if chunked else base), (got, base)
@@ -116,20 +120,22 @@ def _bwd_workspace(T, hq, numseqs, max_len):
     return slots + pair_heads * 2 * 2 * 128 * 128 * 4
 
 
-@pytest.mark.parametrize("T,ns,hq,d,dtype,chunked", [
-    (24576, 11, 2, 128, _capi.DTYPE_BFLOAT16, True),
-    (24576, 11, 2, 64, _capi.DTYPE_BFLOAT16, True),
-    (256 * 128, 3, 2, 128, _capi.DTYPE_BFLOAT16, False),  # the grid cannot be small
-    (24576, 11, 2, 128, _capi.DTYPE_FLOAT32, False),
+@pytest.mark.parametrize("T,total,ns,hq,d,dtype,chunked", [
+    (24576, 24576, 11, 2, 128, _capi.DTYPE_BFLOAT16, True),
+    (24576, 24576, 11, 2, 64, _capi.DTYPE_BFLOAT16, True),
+    (256 * 128, 256 * 128, 3, 2, 128, _capi.DTYPE_BFLOAT16, False),  # the grid cannot be small
+    (256 * 128, 3000, 3, 2, 128, _capi.DTYPE_BFLOAT16, True),        # padded: 3000 real tokens
+    (24576, 24576, 11, 2, 128, _capi.DTYPE_FLOAT32, False),
 ])
-def test_bwd_workspace_with_dq_chunks(lib, T, ns, hq, d, dtype, chunked):
+def test_bwd_workspace_with_dq_chunks(lib, T, total, ns, hq, d, dtype, chunked):
     """dq_key_chunks adds, after the rest of the workspace, the dQ list with room for the parts
     (int4 [cap + 1024 // hq]), one int32 counter per (chunk slot, q head) and the chunk slots;
-    only where the grid can be small (ceil(T / 128) * hq < 512) and for bf16."""
+    only where the grid can be small (ceil(min(T, total_seqlen) / 128) * hq < 512) and for bf16."""
     def align(x):
         return (x + 255) // 256 * 256
     p = _capi.BwdParams()
     p.total_tokens, p.num_q_heads, p.num_kv_heads, p.numseqs, p.max_seqlen_all = T, hq, hq, ns, 4096
+    p.total_seqlen = total
     p.head_dim, p.dtype = d, dtype
     base = lib.mimir_prefixlm_bwd_workspace_size(ctypes.byref(p))
     assert base == _bwd_workspace(T, hq, ns, 4096)

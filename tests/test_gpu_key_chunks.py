@@ -148,6 +148,29 @@ def test_chunked_forward(device, idx, key_chunks):
     assert errs[0] <= 2e-2 and errs[1] <= 1e-2
 
 
+def test_padded_small_grid_is_cut(device, key_chunks):
+    """A padded batch: 3700 real tokens in a 40000-row tensor.  By the tensor's length alone
+    (ceil(40000 / 128) x 2 heads = 626 >= 512 workgroups) the grid could not be small, but its
+    query tiles (29 x 2) are few: the chunk room is sized from min(T, total_seqlen), so the
+    list cuts them; the cut forward matches the oracle and leaves the padding rows zero."""
+    case = make_case([3000, 700], [100, 700], 2, 1, 128, seed=49, dtype=torch.bfloat16, pad_to=40000)
+    c = case.to(device)
+    assert -(-c.T // 128) * 2 >= 512 and -(-int(c.total_seqlen) // 128) * 2 < 512
+    got, cut = forward(c, True, case)
+    print(f"[chunks] padded small grid: {cut} cut list entries", flush=True)
+    assert cut > 0
+    total = int(c.total_seqlen)
+    assert torch.equal(got["o"][total:], torch.zeros_like(got["o"][total:]))
+    assert torch.isneginf(got["lse"][:, total:]).all()
+    qf, kf, vf = (t.float() for t in (case.q, case.k, case.v))
+    args = case.oracle_args()
+    o_ref = dense_forward(qf, kf, vf, case.is_causal, *args)
+    lse_ref = dense_lse(qf, kf, case.is_causal, *args)
+    errs = (close(got["o"].float().cpu(), o_ref), close(got["lse"].float().cpu(), lse_ref))
+    print(f"[chunks] padded small grid: O {errs[0]:.3g} lse {errs[1]:.3g} against the oracle", flush=True)
+    assert errs[0] <= 2e-2 and errs[1] <= 1e-2
+
+
 @pytest.mark.parametrize("split", [_capi.SPLIT_ALWAYS, _capi.SPLIT_NEVER], ids=["split", "plain"])
 def test_chunked_forward_gate_rope(device, split, key_chunks):
     """Gated output, RoPE of q in the kernel (with the rotated q written out) and the P hi + lo

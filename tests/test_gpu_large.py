@@ -29,6 +29,7 @@ Invariants (every bf16 workload):
   active queries of dO, summed over the q-heads of each kv head (rows of P sum to 1).
 """
 
+import dataclasses
 import math
 
 import pytest
@@ -180,5 +181,29 @@ def test_split_decision_on_the_device(device):
                           flush=True)
                     assert r_split <= 1, (name, r_split)
                 assert channel_excess(res["never"][2], ref[2]).max().item() > 1  # dQ needs the split
+    finally:
+        P._split_mode = mode
+
+
+def test_split_decision_ignores_padding_keys(device):
+    """The K scan behind AUTO reads only the keys inside sequences: large values or NaN in the
+    padding rows of K (never attended) change neither the decision nor any output bit (the plain
+    input stays bitwise equal to split mode "never")."""
+    mode = P._split_mode
+    try:
+        case = make_case([1500, 700], [600, 0], 8, 2, 128, seed=31, dtype=torch.bfloat16, pad_to=2400)
+        P.set_split_mode("never")
+        never = run(case, device)
+        P.set_split_mode("auto")
+        clean = run(case, device)
+        for a, b in zip(clean, never):
+            assert torch.equal(a, b)
+        total = sum(case.seq_lens)
+        for fill in (1e4, float("nan")):
+            k = case.k.clone()
+            k[total:] = fill
+            dirty = run(dataclasses.replace(case, k=k), device)
+            for a, b in zip(dirty, clean):
+                assert torch.equal(a, b), fill
     finally:
         P._split_mode = mode
