@@ -159,22 +159,20 @@ def dscore_blocks(case) -> int:
     return total
 
 
-def working_kernels(d: int, elem: int, split: bool, handoff: bool) -> dict:
-    """Full names, as rocprofv3 reports them, of the kernel instantiations that do each stage's work.
+def working_kernels(d: int, elem: int, handoff: bool) -> dict:
+    """Full names, as rocprofv3 reports them, of the kernels that do each stage's work.
 
-    With split_mode AUTO the bf16 stages enqueue a plain and a split instantiation and
-    the one the device-side K scan does not select exits at once; ``split`` says which
-    one works.  ``handoff``: the dK/dV kernel stores dS and dq_ds_kernel reads it.
+    One bf16 kernel serves both split modes (the device-side decision picks the
+    body inside it).  ``handoff``: the dK/dV kernel stores dS and dq_ds_kernel
+    reads it.
     """
     if elem == 4:
         return {"fwd": f"fwd_f32_kernel<{d}>", "dkdv": f"dkdv_f32_kernel<{d}>", "dq": f"dq_f32_kernel<{d}>"}
-    flag = "true" if split else "false"
     if d == 128:
-        dkdv = "dkdv_pair_ds_kernel" if handoff else f"dkdv_pair_kernel<{flag}>"
+        dkdv = "dkdv_pair_ds_kernel" if handoff else "dkdv_pair_kernel"
     else:
-        dkdv = f"dkdv_kernel<{d}, {flag}>"
-    return {"fwd": f"fwd_bf16_kernel<{d}, {int(split)}>", "dkdv": dkdv,
-            "dq": "dq_ds_kernel" if handoff else f"dq_kernel<{d}>"}
+        dkdv = f"dkdv_kernel<{d}>"
+    return {"fwd": f"fwd_bf16_kernel<{d}>", "dkdv": dkdv, "dq": "dq_ds_kernel" if handoff else f"dq_kernel<{d}>"}
 
 
 def _measured_traffic(workload: str, kernel: str):
@@ -183,7 +181,7 @@ def _measured_traffic(workload: str, kernel: str):
     profiles/hbm_traffic.json holds FETCH_SIZE and WRITE_SIZE per dispatch from two
     rocprofv3 --pmc runs of this script, each scaled by what the same counter reads
     for a plain 1 GiB device copy, keyed by the full instantiation name (the plain
-    and split instantiations of one kernel are separate entries); None when the
+    and split bodies share one kernel, so a workload holds one entry per stage); None when the
     workload or the kernel was not profiled.
     """
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
@@ -603,7 +601,7 @@ def main() -> int:
     keys = case.k[cu[0]:cu[int(case.numseqs)]]
     split = elem == 2 and keys.numel() > 0 and bool(keys.float().abs().max().item() * scale > 0.75)
     handoff = handoff and not split
-    kernel_names = working_kernels(d, elem, split, handoff)
+    kernel_names = working_kernels(d, elem, handoff)
     dom = max((n for n in kernel_flops if n in stage_avg), key=lambda n: stage_avg[n])
     achieved = kernel_flops[dom] / (stage_avg[dom] * 1e-3) / 1e12
     alg_bytes = fwd_bytes(T, hq, hkv, d, elem) + (0 if fwd_only else bwd_bytes(T, hq, hkv, d, elem))

@@ -74,14 +74,14 @@ __device__ __forceinline__ bool dq_needs_recompute(const BwdArgs& a, bool split)
 // depend on arrival order.  Returns whether this workgroup stores dQ.  Called
 // by every wave of the workgroup (it holds barriers).
 template <int DT>
-__device__ __forceinline__ bool dq_merge_parts(const BwdArgs& a, int4 item, int h, int wave, int lane,
+__device__ __forceinline__ bool dq_merge_parts(const BwdArgs& a, uint64_t seg, int4 item, int h, int wave, int lane,
                                                f32x16 (&acc)[DT]) {
   __shared__ int later;
   constexpr int kDevScope = 16;  // buffer cache policy: coherent at device scope
   const int part = item.z & 0xffff, parts = item.z >> 16;
   const int slot0 = item.w - part;
   const uint32_t slot_bytes = (uint32_t)chunk_slot_bytes(DT * 32);
-  char* const base = kernarg_at<char*>(offsetof(BwdArgs, chunk_part));
+  char* const base = kernarg_at<char*>(seg, offsetof(BwdArgs, chunk_part));
   auto slot_rsrc = [&](int sl) { return make_rsrc(base + ((size_t)sl * a.Hq + h) * slot_bytes, slot_bytes); };
   auto offset = [&](int dt, int rg) { return (uint32_t)((((wave * DT + dt) * 4 + rg) * 64 + lane) * 16); };
   {
@@ -98,7 +98,7 @@ __device__ __forceinline__ bool dq_merge_parts(const BwdArgs& a, int4 item, int 
   wait_vmem();  // the slot stores are complete
   __syncthreads();
   if (threadIdx.x == 0) {
-    int* const ctr = kernarg_at<int*>(offsetof(BwdArgs, chunk_ctr)) + (size_t)slot0 * a.Hq + h;
+    int* const ctr = kernarg_at<int*>(seg, offsetof(BwdArgs, chunk_ctr)) + (size_t)slot0 * a.Hq + h;
     const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == parts - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     later = prev == parts - 1;

@@ -26,23 +26,37 @@ struct DkCfg {
   static constexpr int kWavesPerSimd = 2;
 };
 
-// kSplit: dS as bf16 hi + lo in the dK product.  With split_mode AUTO both
-// instantiations are enqueued and the one the K scan does not select exits at once.
+// Three LDS stages of (Q tile, dO tile, lse2 row, delta row), each one object,
+// so that the compiler can tell the reads of one stage from the tile copies into
+// another (it tracks the copy targets of a few objects only).  Declared apart
+// from the body, so that the kernel's plain and split bodies share them.
+struct DkStages {
+  bf16_t *s0, *s1, *s2;
+};
+template <int D>
+__device__ __forceinline__ DkStages dk_stages() {
+  constexpr int kStageElems = 2 * TileLayout<D>::kElems + 2 * kBwdBlockQT * 2;  // Q, dO, lse2 + delta (fp32)
+  __shared__ __attribute__((aligned(16))) bf16_t sS0[kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS1[kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS2[kStageElems];
+  return DkStages{sS0, sS1, sS2};
+}
+
+// kSplit: dS as bf16 hi + lo in the dK product (a compile-time choice: it changes
+// the registers of the tile loop; the kernel below calls the split body as a
+// function of its own).
 template <int D, bool kSplit>
-__global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) void dkdv_kernel(const BwdArgs a) {
+__device__ __forceinline__ void dkdv_body(const BwdArgs& a) {
   constexpr int DT = D / 32;
   constexpr int KS = D / 16;
   constexpr int kDkWaves = DkCfg<D>::kWaves;
   constexpr int kDkKeys = DkCfg<D>::kKeys;
   using L = TileLayout<D>;
   static_assert(kBwdBlockQT == 64, "one TileLayout tile per Q / dO block");
-  // Three LDS stages of (Q tile, dO tile, lse2 row, delta row), each one
-  // object, so that the compiler can tell the reads of one stage from the
-  // tile copies into another (it tracks the copy targets of a few objects only).
-  constexpr int kStageElems = 2 * L::kElems + 2 * kBwdBlockQT * 2;  // Q, dO, then lse2 and delta (fp32)
-  __shared__ __attribute__((aligned(16))) bf16_t sS0[kStageElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sS1[kStageElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sS2[kStageElems];
+  const DkStages st = dk_stages<D>();
+  bf16_t* const sS0 = st.s0;
+  bf16_t* const sS1 = st.s1;
+  bf16_t* const sS2 = st.s2;
   bf16_t* const sQ0 = sS0;
   bf16_t* const sO0 = sS0 + L::kElems;
   float* const sL0 = (float*)(sS0 + 2 * L::kElems);
@@ -292,20 +306,33 @@ __global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) voi
 }
 
 
-template __global__ void dkdv_kernel<64, false>(const BwdArgs);
-template __global__ void dkdv_kernel<64, true>(const BwdArgs);
+// The split body in a function of its own, which the kernel calls when the split
+// is on: the plain body, inlined in the kernel, keeps the registers and code of a
+// kernel of its own.  It reads its arguments from the kernel's argument segment
+// `seg`.
+template <int D>
+__device__ __attribute__((noinline)) void dkdv_split_body(uint64_t seg) {
+  dkdv_body<D, true>(segment_args<BwdArgs>(uniform_segment(seg)));
+}
+// One launch for every split mode: the decision (the forward's recorded one, or
+// the K scan's) picks the body.
+template <int D>
+__global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) void dkdv_kernel(const BwdArgs a) {
+  if (split_on(a, threadIdx.x & 63))
+    dkdv_split_body<D>(kernel_segment());
+  else
+    dkdv_body<D, false>(a);
+}
+template __global__ void dkdv_kernel<64>(const BwdArgs);
 
 template <int D>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   constexpr int kDkKeys = DkCfg<D>::kKeys, kDkWaves = DkCfg<D>::kWaves;
   static_assert(kDkKeys == kPlanTile, "work-list tiles are the dK / dV key tiles");
   if (numseqs <= 0 || a.cap_k == 0) return hipSuccess;
-  // workgroup r * Hkv + h: list entry r, kv head h; AUTO enqueues both instantiations
+  // workgroup r * Hkv + h: list entry r, kv head h
   const dim3 grid((unsigned)a.cap_k * (unsigned)a.Hkv);
-  void (*const plain)(BwdArgs) = dkdv_kernel<D, false>;
-  void (*const split)(BwdArgs) = dkdv_kernel<D, true>;
-  if (a.split_mode != MIMIR_SPLIT_ALWAYS) hipLaunchKernelGGL(plain, grid, dim3(kDkWaves * 64), 0, stream, a);
-  if (a.split_mode != MIMIR_SPLIT_NEVER) hipLaunchKernelGGL(split, grid, dim3(kDkWaves * 64), 0, stream, a);
+  hipLaunchKernelGGL(dkdv_kernel<D>, grid, dim3(kDkWaves * 64), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -28,8 +28,31 @@ constexpr int kNonTemporal = 2;  // buffer cache policy: streaming (nt)
 constexpr int kPairKeys = 128;
 constexpr int kPairD = 128;
 
+// LDS: three stages of (Q tile, dO tile, lse2 row, delta row) and the V tile
+// (two 64-row TileLayout tiles).  Each stage is one object, so that the
+// compiler can tell the reads of one stage from the tile copies into another (it
+// tracks the copy targets of a few objects only: with one object per tile it
+// made some stage's reads wait for every copy in flight).  Declared apart from
+// the body, so that a kernel's plain and split bodies share them.  After the
+// tile loop the Q / dO tiles of stages 0 and 1 hold the dK / dV partials of the
+// second wave of each pair.
+constexpr int kStageElems = 2 * TileLayout<kPairD>::kElems + 2 * kBwdBlockQT * 2;  // Q, dO, lse2 + delta (fp32)
+struct PairLds {
+  bf16_t *s0, *s1, *s2, *v;
+  int *unit_next, *later;
+};
+__device__ __forceinline__ PairLds pair_lds() {
+  __shared__ __attribute__((aligned(16))) bf16_t sS0[kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS1[kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sS2[kStageElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV[2 * TileLayout<kPairD>::kElems];
+  __shared__ int unit_next;
+  __shared__ int later;
+  return PairLds{sS0, sS1, sS2, sV, &unit_next, &later};
+}
+
 template <bool kStoreDs, bool kSplit>
-__device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
+__device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a, uint64_t seg) {
   constexpr int D = kPairD;
   constexpr int DT = D / 32;
   constexpr int KS = D / 16;
@@ -37,18 +60,13 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   using Loader = TileLoader<D, kPairWaves>;
   static_assert(kBwdBlockQT == 64, "one TileLayout tile per Q / dO block");
 
-  // LDS: three stages of (Q tile, dO tile, lse2 row, delta row) and the V tile
-  // (two 64-row TileLayout tiles).  Each stage is one object, so that the
-  // compiler can tell the reads of one stage from the tile copies into another
-  // (it tracks the copy targets of a few objects only: with one object per
-  // tile it made some stage's reads wait for every copy in flight).  After the
-  // tile loop the Q / dO tiles of stages 0 and 1 hold the dK / dV partials of
-  // the second wave of each pair.
-  constexpr int kStageElems = 2 * L::kElems + 2 * kBwdBlockQT * 2;  // Q, dO, then lse2 and delta (fp32)
-  __shared__ __attribute__((aligned(16))) bf16_t sS0[kStageElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sS1[kStageElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sS2[kStageElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[2 * L::kElems];
+  const PairLds lds = pair_lds();
+  bf16_t* const sS0 = lds.s0;
+  bf16_t* const sS1 = lds.s1;
+  bf16_t* const sS2 = lds.s2;
+  bf16_t* const sV = lds.v;
+  int& unit_next = *lds.unit_next;  // the workgroup's next work unit
+  int& later = *lds.later;          // split tiles: 1 if this half arrived second
   bf16_t* const sQ0 = sS0;
   bf16_t* const sO0 = sS0 + L::kElems;
   float* const sL0 = (float*)(sS0 + 2 * L::kElems);
@@ -63,9 +81,6 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   float* const sD2 = sL2 + kBwdBlockQT;
   static_assert(64 * 64 * 4 <= L::kElems * 2, "one slice's partials fit one tile object");
 
-  __shared__ int unit_next;  // the workgroup's next work unit
-  __shared__ int later;      // split tiles: 1 if this half arrived second
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -76,8 +91,7 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   const Loader ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane), ldv(a.v_st, wave, lane);
   const TileLanes<D> tl(lane);
   const float c2 = a.scale_log2;
-  // kSplit: dS as bf16 hi + lo in the dK product.  With split_mode AUTO both
-  // instantiations are enqueued and the one the K scan does not select exits here.
+  // kSplit: dS as bf16 hi + lo in the dK product (the kernels pick the body).
   if (split_on(a, lane) != kSplit) return;
   auto fetch_unit = [&]() {  // next work unit from the launch-wide queue
     return (int)gridDim.x + __hip_atomic_fetch_add(&a.queue[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -273,10 +287,10 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     if constexpr (kStoreDs) {
       const int row = ds_row0 + (qr >> 5);
       // region geometry loaded per step: no scalar registers held across the loop
-      const int64_t blk = ((int64_t)(hk * a.group + head) * kernarg_at<int>(offsetof(BwdArgs, ds_rows)) + row) *
-                              kernarg_at<int>(offsetof(BwdArgs, ds_width)) +
+      const int64_t blk = ((int64_t)(hk * a.group + head) * kernarg_at<int>(seg, offsetof(BwdArgs, ds_rows)) + row) *
+                              kernarg_at<int>(seg, offsetof(BwdArgs, ds_width)) +
                           (ka >> 5);
-      rds = make_rsrc(kernarg_at<bf16_t*>(offsetof(BwdArgs, dscore)) + blk * kDsBlockElems,
+      rds = make_rsrc(kernarg_at<bf16_t*>(seg, offsetof(BwdArgs, dscore)) + blk * kDsBlockElems,
                       ds_unit_ok ? kDsBlockElems * 2 : 0);
     }
     auto store_ds = [&](int s2) {
@@ -402,8 +416,8 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
     constexpr int kDevScope = 16;  // buffer cache policy: coherent at device scope
     constexpr uint32_t kSliceBytes = DT * 4 * 64 * 16;
     const int ph = item.w * a.Hkv + hk;
-    float* const split_buf = kernarg_at<float*>(offsetof(BwdArgs, split_buf));
-    int* const split_ctr = kernarg_at<int*>(offsetof(BwdArgs, split_ctr));
+    float* const split_buf = kernarg_at<float*>(seg, offsetof(BwdArgs, split_buf));
+    int* const split_ctr = kernarg_at<int*>(seg, offsetof(BwdArgs, split_ctr));
     const float* const slot_mine = split_buf + ((size_t)ph * 2 + (half - 1)) * kSplitSlotFloats;
     const float* const slot_other = split_buf + ((size_t)ph * 2 + (2 - half)) * kSplitSlotFloats;
     if (qh == 0) {
@@ -462,12 +476,12 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   const int kpos = ka + l32;
   if (kpos >= g.n) return;
   // the destinations loaded here: no scalar registers held across the tile loop
-  bf16_t* krow = kernarg_at<bf16_t*>(offsetof(BwdArgs, dk)) +
-                 (int64_t)(g.start + kpos) * kernarg_at<int64_t>(offsetof(BwdArgs, dk_st)) +
-                 (int64_t)hk * kernarg_at<int64_t>(offsetof(BwdArgs, dk_sh));
-  bf16_t* vrow = kernarg_at<bf16_t*>(offsetof(BwdArgs, dv)) +
-                 (int64_t)(g.start + kpos) * kernarg_at<int64_t>(offsetof(BwdArgs, dv_st)) +
-                 (int64_t)hk * kernarg_at<int64_t>(offsetof(BwdArgs, dv_sh));
+  bf16_t* krow = kernarg_at<bf16_t*>(seg, offsetof(BwdArgs, dk)) +
+                 (int64_t)(g.start + kpos) * kernarg_at<int64_t>(seg, offsetof(BwdArgs, dk_st)) +
+                 (int64_t)hk * kernarg_at<int64_t>(seg, offsetof(BwdArgs, dk_sh));
+  bf16_t* vrow = kernarg_at<bf16_t*>(seg, offsetof(BwdArgs, dv)) +
+                 (int64_t)(g.start + kpos) * kernarg_at<int64_t>(seg, offsetof(BwdArgs, dv_st)) +
+                 (int64_t)hk * kernarg_at<int64_t>(seg, offsetof(BwdArgs, dv_sh));
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -477,7 +491,7 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
       for (int e = 0; e < 4; ++e) tv[e] = dvacc[dt][4 * rg + e];
       *(bf16x4*)&vrow[32 * dt + 8 * rg + 4 * hi] = __builtin_convertvector(tv, bf16x4);
     }
-  grad_out<DT>(dkacc, kernarg_at<float>(offsetof(BwdArgs, scale)), rope_at(offsetof(BwdArgs, rope)),
+  grad_out<DT>(dkacc, kernarg_at<float>(seg, offsetof(BwdArgs, scale)), rope_at(seg, offsetof(BwdArgs, rope)),
                g.start + kpos, hi,
                [&](int dt, int rg, bf16x4 v) { *(bf16x4*)&krow[32 * dt + 8 * rg + 4 * hi] = v; });
   };
@@ -507,13 +521,29 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a) {
   }
 }
 
-template <bool kSplit>
-__global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const BwdArgs a) {
-  dkdv_pair_body<false, kSplit>(a);
+// The split body in a function of its own, which both kernels call when the
+// split is on: the plain body, inlined in the kernel, keeps the registers and
+// code of a kernel of its own.  It reads its arguments from the kernel's
+// argument segment `seg` (a reference to the kernel's by-value argument would
+// make the compiler copy it to the stack for both bodies).  The hand-off
+// stores unsplit dS only: with a split dQ the stored tiles are not used.
+__device__ __attribute__((noinline)) void dkdv_pair_split_body(uint64_t seg) {
+  seg = uniform_segment(seg);
+  dkdv_pair_body<false, true>(segment_args<BwdArgs>(seg), seg);
 }
-// The hand-off stores unsplit dS: with a split dQ the stored tiles are not used.
+// One launch for every split mode: the decision (the forward's recorded one, or
+// the K scan's) picks the body.
+__global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const BwdArgs a) {
+  if (split_on(a, threadIdx.x & 63))
+    dkdv_pair_split_body(kernel_segment());
+  else
+    dkdv_pair_body<false, false>(a, kernel_segment());
+}
 __global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_ds_kernel(const BwdArgs a) {
-  dkdv_pair_body<true, false>(a);
+  if (split_on(a, threadIdx.x & 63))
+    dkdv_pair_split_body(kernel_segment());
+  else
+    dkdv_pair_body<true, false>(a, kernel_segment());
 }
 
 }  // namespace
@@ -526,14 +556,8 @@ hipError_t launch_bwd_dkdv_pair_bf16(BwdArgs a, int numseqs, int max_seqlen_all,
   // one persistent workgroup per CU
   const int64_t units = (int64_t)a.cap_k * a.Hkv;
   const int grid = (int)(units < device_cu_count() ? units : device_cu_count());
-  // AUTO: the unsplit and the split instantiation, each exiting at once unless the
-  // K scan selects it (the persistent grid is one workgroup per CU, so the
-  // exiting one costs a few microseconds)
-  if (a.split_mode != MIMIR_SPLIT_ALWAYS)
-    hipLaunchKernelGGL(a.dscore != nullptr ? dkdv_pair_ds_kernel : dkdv_pair_kernel<false>, dim3((unsigned)grid),
-                       dim3(kPairWaves * 64), 0, stream, a);
-  if (a.split_mode != MIMIR_SPLIT_NEVER)
-    hipLaunchKernelGGL(dkdv_pair_kernel<true>, dim3((unsigned)grid), dim3(kPairWaves * 64), 0, stream, a);
+  hipLaunchKernelGGL(a.dscore != nullptr ? dkdv_pair_ds_kernel : dkdv_pair_kernel, dim3((unsigned)grid),
+                     dim3(kPairWaves * 64), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -188,7 +188,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   }
 
   // A part of a cut key range: the last part of the tile to arrive sums them.
-  if (__builtin_expect(parts > 1, 0) && !dq_merge_parts<DT>(a, item, h, wave, lane, dqacc)) return;
+  if (__builtin_expect(parts > 1, 0) && !dq_merge_parts<DT>(a, kernel_segment(), item, h, wave, lane, dqacc)) return;
 
   // Epilogue: each wave stages its 32 dQ rows in LDS (one K / V stage object
   // per wave, free once every wave is past the tile loop) and stores whole

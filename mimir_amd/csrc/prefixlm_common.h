@@ -194,22 +194,23 @@ struct RopeTab {
   int64_t st;        // elements between the rows of cos / sin
 };
 
-// A field of the kernel's argument struct (the kernel's only parameter, at the
-// start of the kernarg segment), loaded where it is used: the segment pointer
-// is opaque to the compiler, so the scalar load is not hoisted and the value
-// holds no scalar registers across a tile loop (where it would be spilled).
+// A field of the argument struct at the start of the kernel argument segment
+// `seg` (kernel_segment() / uniform_segment()), loaded where it is used: the
+// pointer is opaque to the compiler, so the scalar load is not hoisted and the
+// value holds no scalar registers across a tile loop (where it would be
+// spilled).
 template <typename T>
-__device__ __forceinline__ T kernarg_at(size_t offset) {
+__device__ __forceinline__ T kernarg_at(uint64_t seg, size_t offset) {
   typedef const __attribute__((address_space(4))) char* KPtr;
-  KPtr p = (KPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  KPtr p = (KPtr)seg;
   __asm__ volatile("" : "+s"(p));
   return *(const __attribute__((address_space(4))) T*)(p + offset);
 }
 // The RoPE tables of the argument struct at `offset`, loaded the same way.
-__device__ __forceinline__ RopeTab rope_at(size_t offset) {
-  return RopeTab{kernarg_at<const float*>(offset + offsetof(RopeTab, cos)),
-                 kernarg_at<const float*>(offset + offsetof(RopeTab, sin)),
-                 kernarg_at<int64_t>(offset + offsetof(RopeTab, st))};
+__device__ __forceinline__ RopeTab rope_at(uint64_t seg, size_t offset) {
+  return RopeTab{kernarg_at<const float*>(seg, offset + offsetof(RopeTab, cos)),
+                 kernarg_at<const float*>(seg, offset + offsetof(RopeTab, sin)),
+                 kernarg_at<int64_t>(seg, offset + offsetof(RopeTab, st))};
 }
 
 // Rotation of four column pairs (d1 + e, d1 + e + half), e < 4, of token t.
@@ -631,6 +632,24 @@ __device__ __forceinline__ bool split_decision(int mode, const int* slots, const
   const i32x4 a = ((const i32x4*)slots)[lane], b = ((const i32x4*)slots)[lane + 64];
   const int any = (a[0] | a[1] | a[2] | a[3] | b[0] | b[1] | b[2] | b[3]) != 0;
   return __builtin_amdgcn_ballot_w64(any) != 0;
+}
+
+// The running kernel's argument segment as an integer.  A function the kernel
+// calls gets it as an argument (outside a kernel the segment-pointer builtin
+// reads as null) and passes it through uniform_segment(), which puts it back in
+// scalar registers; segment_args() then reads the struct at its start through a
+// constant-space pointer, with scalar loads as the kernel does.
+__device__ __forceinline__ uint64_t kernel_segment() {
+  return (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
+}
+__device__ __forceinline__ uint64_t uniform_segment(uint64_t seg) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)seg);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(seg >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+template <typename Args>
+__device__ __forceinline__ const Args& segment_args(uint64_t seg) {
+  return *(const Args*)(const __attribute__((address_space(4))) Args*)seg;
 }
 
 // bf16 hi + lo halves of 8 fp32 values: hi = round(x), lo = round(x - hi).

@@ -66,12 +66,14 @@ struct FwdArgs {
 // Two LDS stages of one K tile and one V tile each.  Separate objects let the
 // compiler see that reads of one stage never alias the loads into the other;
 // declared apart from the tile loop's body so that both of a kernel's bodies
-// (split and plain P) use the same LDS.
+// (split and plain P) use the same LDS.  One set per kernel (kGated): objects
+// that the called split body shares with one kernel only sit at fixed
+// addresses, where objects shared by two kernels are found through a table.
 template <int D>
 struct FwdStages {
   bf16_t *k0, *v0, *k1, *v1;
 };
-template <int D>
+template <int D, int kGated>
 __device__ __forceinline__ FwdStages<D> fwd_stages() {
   using L = TileLayout<D>;
   __shared__ __attribute__((aligned(16))) bf16_t sK0[L::kElems];
@@ -82,18 +84,17 @@ __device__ __forceinline__ FwdStages<D> fwd_stages() {
 }
 
 // kSplit: P is not (0) / is (1) split.  The split changes the registers of the
-// tile loop, so it is a compile-time choice: split_mode AUTO enqueues both
-// instantiations and the one the K scan does not select exits at once.  (One
-// kernel holding both bodies behind a uniform branch was measured: with the two
-// bodies in one function the plain one ran 10-17% slower.)
+// tile loop, so it is a compile-time choice; the kernel calls the split body as
+// a function of its own (fwd_split_body).  (Both bodies inlined in one function,
+// behind a uniform branch, made the plain one 10-17% slower.)
 template <int D, int kGated, int kSplit>
-__device__ __forceinline__ void fwd_body(const FwdArgs& a) {
+__device__ __forceinline__ void fwd_body(const FwdArgs& a, uint64_t seg) {
   constexpr int DT = D / 32;  // 32-row d tiles of O^T
   constexpr int KS = D / 16;  // k-steps of S^T = K Q^T
 
   using L = TileLayout<D>;
   static_assert(kBlockN == 64, "one TileLayout tile per K / V block");
-  const FwdStages<D> stages = fwd_stages<D>();
+  const FwdStages<D> stages = fwd_stages<D, kGated>();
   bf16_t* const sK0 = stages.k0;
   bf16_t* const sV0 = stages.v0;
   bf16_t* const sK1 = stages.k1;
@@ -175,7 +176,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   // of the same lane.  Rows past the sequence read the last token's tables and
   // are never stored.
   if (a.rope.cos != nullptr) {
-    const RopeTab rope = rope_at(offsetof(FwdArgs, rope));
+    const RopeTab rope = rope_at(seg, offsetof(FwdArgs, rope));
     const int64_t t = min(g.start + qpos, a.T - 1);
 #pragma unroll
     for (int ks = 0; ks < KS / 2; ++ks) {
@@ -451,10 +452,10 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   }
   // The rotated Q rows (RoPE in the kernel) for the backward: another round
   // through the staging rows, whole rows per store as for O.
-  bf16_t* const q_rope = kernarg_at<bf16_t*>(offsetof(FwdArgs, q_rope));
+  bf16_t* const q_rope = kernarg_at<bf16_t*>(seg, offsetof(FwdArgs, q_rope));
   if (q_rope != nullptr) {
-    const int64_t qr_st = kernarg_at<int64_t>(offsetof(FwdArgs, qr_st));
-    const int64_t qr_sh = kernarg_at<int64_t>(offsetof(FwdArgs, qr_sh));
+    const int64_t qr_st = kernarg_at<int64_t>(seg, offsetof(FwdArgs, qr_st));
+    const int64_t qr_sh = kernarg_at<int64_t>(seg, offsetof(FwdArgs, qr_sh));
     __asm__ volatile("" ::: "memory");
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) *(bf16x8*)&stage[l32 * kPitch + 16 * ks + 8 * hi] = qf[ks];
@@ -495,15 +496,38 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a) {
   }
 }
 
-// Plain and gated stores are separate kernels, so that the gate's pointers stay
-// out of the plain kernel's scalar registers.
-template <int D, int kSplit>
-__global__ __launch_bounds__(kThreads, 2) void fwd_bf16_kernel(const FwdArgs a) {
-  fwd_body<D, 0, kSplit>(a);
+// The split body (P as bf16 hi + lo) in a function of its own, which the kernel
+// calls when the split is on: the plain body, inlined in the kernel, keeps the
+// registers and code of a kernel of its own.  It reads its arguments from the
+// kernel's argument segment `seg` (a reference to the kernel's by-value
+// argument would make the compiler copy it to the stack for both bodies).
+template <int D, int kGated>
+__device__ __attribute__((noinline)) void fwd_split_body(uint64_t seg) {
+  seg = uniform_segment(seg);
+  fwd_body<D, kGated, 1>(segment_args<FwdArgs>(seg), seg);
 }
-template <int D, int kSplit>
-__global__ __launch_bounds__(kThreads, 2) void fwd_bf16_gated_kernel(const FwdArgs a) {
-  fwd_body<D, 1, kSplit>(a);
+// One launch for every split mode: the decision (the K scan's with AUTO) picks
+// the body.  Plain and gated stores are separate kernels, so that the gate's
+// pointers stay out of the plain kernel's scalar registers.
+template <int D, int kGated>
+__device__ __forceinline__ void fwd_kernel_body(const FwdArgs& a) {
+  if (split_decision(a.split_mode, a.kscan, nullptr, threadIdx.x & 63))
+    fwd_split_body<D, kGated>(kernel_segment());
+  else
+    fwd_body<D, kGated, 0>(a, kernel_segment());
+}
+// Workgroups per CU the register budget must allow (LDS allows at least that
+// many): head_dim 64 runs four (gated: three), head_dim 128 two; the called
+// split body gets the same budget.
+template <int D, int kGated>
+constexpr int kFwdWgPerCu = D == 64 ? (kGated ? 3 : 4) : 2;
+template <int D>
+__global__ __launch_bounds__(kThreads, (kFwdWgPerCu<D, 0>)) void fwd_bf16_kernel(const FwdArgs a) {
+  fwd_kernel_body<D, 0>(a);
+}
+template <int D>
+__global__ __launch_bounds__(kThreads, (kFwdWgPerCu<D, 1>)) void fwd_bf16_gated_kernel(const FwdArgs a) {
+  fwd_kernel_body<D, 1>(a);
 }
 
 template <int D>
@@ -581,10 +605,8 @@ hipError_t launch(const MimirPrefixLMFwdParams& p, Prologue pro, hipStream_t str
   // the last unit exit at once.
   const int64_t units = (int64_t)cap * p.num_kv_heads;
   const dim3 grid((unsigned)(((units + kXcds - 1) / kXcds) * kXcds * a.group));
-  void (*const plain)(FwdArgs) = a.gate != nullptr ? fwd_bf16_gated_kernel<D, 0> : fwd_bf16_kernel<D, 0>;
-  void (*const split)(FwdArgs) = a.gate != nullptr ? fwd_bf16_gated_kernel<D, 1> : fwd_bf16_kernel<D, 1>;
-  if (p.split_mode != MIMIR_SPLIT_ALWAYS) hipLaunchKernelGGL(plain, grid, dim3(kThreads), 0, stream, a);
-  if (p.split_mode != MIMIR_SPLIT_NEVER) hipLaunchKernelGGL(split, grid, dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(a.gate != nullptr ? fwd_bf16_gated_kernel<D> : fwd_bf16_kernel<D>, grid, dim3(kThreads), 0,
+                     stream, a);
   return hipGetLastError();
 }
 
