@@ -159,6 +159,16 @@ def dscore_blocks(case) -> int:
     return total
 
 
+def auto_split(case, scale: float) -> bool:
+    """The device-side AUTO rule (softmax_scale * max|K| > 0.75 over the keys inside
+    sequences) on the host copy of K: whether the bf16 kernels carry P and dS split."""
+    if case.k.element_size() != 2:
+        return False
+    cu = case.cu_seqlens.tolist()
+    keys = case.k[cu[0]:cu[int(case.numseqs)]]
+    return keys.numel() > 0 and bool(keys.float().abs().max().item() * scale > 0.75)
+
+
 def working_kernels(d: int, elem: int, handoff: bool) -> dict:
     """Full names, as rocprofv3 reports them, of the kernels that do each stage's work.
 
@@ -595,11 +605,8 @@ def main() -> int:
     peak = PEAK_F32_TFLOPS if c.q.dtype == torch.float32 else PEAK_BF16_TFLOPS
     kernel_flops = {"fwd": f_fwd, "dkdv": 8.0 * d * hq * pairs, "dq": 2.0 * d * hq * pairs}
     handoff = not fwd_only and int(lib.mimir_prefixlm_bwd_dscore_bytes(bpr)) > 0  # dQ reads dK/dV's dS
-    # the device-side AUTO rule (softmax_scale * max|K| > 0.75, over the keys inside sequences) on the
-    # host copy of K: with the split the recomputing dQ does the work even where the hand-off region exists
-    cu = case.cu_seqlens.tolist()
-    keys = case.k[cu[0]:cu[int(case.numseqs)]]
-    split = elem == 2 and keys.numel() > 0 and bool(keys.float().abs().max().item() * scale > 0.75)
+    # with the split the recomputing dQ does the work even where the hand-off region exists
+    split = auto_split(case, scale)
     handoff = handoff and not split
     kernel_names = working_kernels(d, elem, handoff)
     dom = max((n for n in kernel_flops if n in stage_avg), key=lambda n: stage_avg[n])

@@ -39,3 +39,58 @@ def _brute_force_blocks(case) -> int:
 def test_dscore_blocks_match_the_mask(seq_lens, prefixes, causal):
     case = make_case(seq_lens, prefixes, 2, 1, 64, seed=0, is_causal=causal)
     assert bench.dscore_blocks(case) == _brute_force_blocks(case)
+
+
+def _dscore_region(lib, case, limit: int) -> int:
+    """The library's hand-off region for the case's sizes (0: dQ recomputes)."""
+    import ctypes
+
+    from mimir_amd import _capi
+
+    p = _capi.BwdParams()
+    T, hq, d = case.q.shape
+    p.total_tokens, p.num_q_heads, p.num_kv_heads = T, hq, case.k.shape[1]
+    p.numseqs, p.max_seqlen_all = int(case.numseqs), int(case.max_seqlen_all)
+    p.head_dim = d
+    p.dtype = _capi.DTYPE_BFLOAT16 if case.q.element_size() == 2 else _capi.DTYPE_FLOAT32
+    p.dscore_limit_bytes = limit
+    return int(lib.mimir_prefixlm_bwd_dscore_bytes(ctypes.byref(p)))
+
+
+def test_traffic_profile_holds_the_working_kernels():
+    """profiles/hbm_traffic.json (what bench.py reports as roofline.traffic) holds, for every
+    profiled workload, an entry for each kernel that does a stage's work -- the names bench.py
+    looks up -- and each entry is at least the bytes that kernel must move: its outputs
+    plus one read of the operands it cannot skip.  (An entry of a kernel that exited at once
+    holds a few KB and fails this.)"""
+    import json
+    import math
+
+    from mimir_amd import _capi
+    from mimir_amd import prefixlm as P
+    from mimir_amd.workloads import CONFIG_NAMES, make_config
+
+    data = json.loads((Path(__file__).resolve().parents[1] / "profiles" / "hbm_traffic.json").read_text())
+    lib = _capi.load()
+    recompute_tag = " (dQ recomputes: no dS hand-off)"
+    by_name = {v: k for k, v in CONFIG_NAMES.items()}
+    seen = set()
+    for name, entries in data["workloads"].items():
+        base = name[: -len(recompute_tag)] if name.endswith(recompute_tag) else name
+        idx = by_name[base]
+        seen.add(idx)
+        case = make_config(idx, seed=0)
+        T, hq, d = case.q.shape
+        hkv, elem = case.k.shape[1], case.q.element_size()
+        scale = 1.0 / math.sqrt(d)
+        limit = 0 if name.endswith(recompute_tag) else P._dscore_limit_bytes
+        handoff = _dscore_region(lib, case, limit) > 0 and not bench.auto_split(case, scale)
+        names = bench.working_kernels(d, elem, handoff)
+        q_bytes, kv_bytes = T * hq * d * elem, T * hkv * d * elem
+        floor = {"fwd": 2 * q_bytes + 2 * kv_bytes,  # Q, K, V read, O written
+                 "dkdv": 2 * q_bytes + 4 * kv_bytes,  # Q, dO, K, V read, dK, dV written
+                 "dq": q_bytes + kv_bytes}  # K read, dQ written
+        for stage, kernel in names.items():
+            assert kernel in entries, f"{name}: no entry for {kernel}"
+            assert entries[kernel]["bytes"] >= floor[stage], f"{name}: {kernel} {entries[kernel]['bytes']} B"
+    assert seen == {2, 3, 4, 5, 6}
