@@ -315,9 +315,12 @@ __device__ __attribute__((noinline)) void dkdv_split_body(uint64_t seg) {
   dkdv_body<D, true>(segment_args<BwdArgs>(uniform_segment(seg)));
 }
 // One launch for every split mode: the decision (the forward's recorded one, or
-// the K scan's) picks the body.
+// the K scan's) picks the body.  The waves per SIMD are pinned as the least and
+// the most, so that the called body is scheduled for that occupancy too.
 template <int D>
-__global__ __launch_bounds__(DkCfg<D>::kWaves * 64, DkCfg<D>::kWavesPerSimd) void dkdv_kernel(const BwdArgs a) {
+__global__ __attribute__((amdgpu_flat_work_group_size(DkCfg<D>::kWaves * 64, DkCfg<D>::kWaves * 64),
+                          amdgpu_waves_per_eu(DkCfg<D>::kWavesPerSimd, DkCfg<D>::kWavesPerSimd))) void dkdv_kernel(
+    const BwdArgs a) {
   if (split_on(a, threadIdx.x & 63))
     dkdv_split_body<D>(kernel_segment());
   else

@@ -249,8 +249,7 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a, uint64_t seg) {
       }
     };
 
-    // S / dP MFMAs at raised wave priority: of the two waves on a SIMD, the one
-    // ready to issue MFMAs goes first while the other runs its softmax.
+    // S / dP MFMAs, their operands read two k-steps ahead.
     rd_a(0);
     rd_a(1);
 #pragma unroll
@@ -532,14 +531,17 @@ __device__ __attribute__((noinline)) void dkdv_pair_split_body(uint64_t seg) {
   dkdv_pair_body<false, true>(segment_args<BwdArgs>(seg), seg);
 }
 // One launch for every split mode: the decision (the forward's recorded one, or
-// the K scan's) picks the body.
-__global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_kernel(const BwdArgs a) {
+// the K scan's) picks the body.  Two waves per SIMD, pinned as the least and
+// the most so that the called body is scheduled for that occupancy too.
+#define MIMIR_PAIR_LAUNCH \
+  __attribute__((amdgpu_flat_work_group_size(kPairWaves * 64, kPairWaves * 64), amdgpu_waves_per_eu(2, 2)))
+__global__ MIMIR_PAIR_LAUNCH void dkdv_pair_kernel(const BwdArgs a) {
   if (split_on(a, threadIdx.x & 63))
     dkdv_pair_split_body(kernel_segment());
   else
     dkdv_pair_body<false, false>(a, kernel_segment());
 }
-__global__ __launch_bounds__(kPairWaves * 64, 2) void dkdv_pair_ds_kernel(const BwdArgs a) {
+__global__ MIMIR_PAIR_LAUNCH void dkdv_pair_ds_kernel(const BwdArgs a) {
   if (split_on(a, threadIdx.x & 63))
     dkdv_pair_split_body(kernel_segment());
   else

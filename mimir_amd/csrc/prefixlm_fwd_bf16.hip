@@ -516,17 +516,22 @@ __device__ __forceinline__ void fwd_kernel_body(const FwdArgs& a) {
   else
     fwd_body<D, kGated, 0>(a, kernel_segment());
 }
-// Workgroups per CU the register budget must allow (LDS allows at least that
-// many): head_dim 64 runs four (gated: three), head_dim 128 two; the called
-// split body gets the same budget.
+// Waves per SIMD (= workgroups per CU) the kernel runs at: head_dim 64 four
+// (gated: three), head_dim 128 two.  Pinned as both the least and the most: the
+// register budget must allow that many, and the called split body, whose
+// occupancy the compiler cannot bound by the kernel's LDS, is scheduled for
+// the same count (with only the least given it aimed at more waves and
+// serialized its LDS operand reads to save registers).
 template <int D, int kGated>
-constexpr int kFwdWgPerCu = D == 64 ? (kGated ? 3 : 4) : 2;
+constexpr int kFwdWaves = D == 64 ? (kGated ? 3 : 4) : 2;
 template <int D>
-__global__ __launch_bounds__(kThreads, (kFwdWgPerCu<D, 0>)) void fwd_bf16_kernel(const FwdArgs a) {
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(kFwdWaves<D, 0>, kFwdWaves<D, 0>))) void fwd_bf16_kernel(const FwdArgs a) {
   fwd_kernel_body<D, 0>(a);
 }
 template <int D>
-__global__ __launch_bounds__(kThreads, (kFwdWgPerCu<D, 1>)) void fwd_bf16_gated_kernel(const FwdArgs a) {
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(kFwdWaves<D, 1>, kFwdWaves<D, 1>))) void fwd_bf16_gated_kernel(const FwdArgs a) {
   fwd_kernel_body<D, 1>(a);
 }
 
