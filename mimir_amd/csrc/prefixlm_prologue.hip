@@ -45,6 +45,7 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kPlanBuckets = 4096;  // costs above kPlanBuckets - 1 share the last bucket
 constexpr int kBucketsPerThread = kPlanBuckets / kThreads;
 constexpr int kFillRows = 16;
+constexpr int kFillWgs = 128;  // fill workgroups per target, at most
 
 struct PrologueArgs {
   PlanArgs plan[2];
@@ -451,25 +452,31 @@ __device__ void kscan_block(const KScanArgs& a, int b) {
   if (threadIdx.x == 0) a.slots[b] = any ? 1 : 0;
 }
 
-// Zeroes the padding rows among packed rows [16 b, 16 b + 16) of one tensor.
-__device__ void fill_block(const FillArgs& a, int b) {
-  const int t0 = b * kFillRows;
-  const int first = a.numseqs > 0 ? a.cu_seqlens[0] : a.T;
+// Zeroes the padding rows of one tensor: the rows t < first or t >= last of
+// the packed rows, first = cu_seqlens[0], last = min(cu_seqlens[numseqs],
+// total_seqlen).  The fill_blocks workgroups of the target take 16-row chunks
+// of those rows in turn, so a batch without padding costs one bounded set of
+// workgroups that exit at once, not one per 16 rows of T.
+__device__ void fill_block(const FillArgs& a, int b, int fill_blocks) {
+  int first = a.numseqs > 0 ? a.cu_seqlens[0] : a.T;
   int last = a.numseqs > 0 ? a.cu_seqlens[a.numseqs] : 0;
+  first = first < 0 ? 0 : (first > a.T ? a.T : first);
   if (last > a.total_seqlen) last = a.total_seqlen;
-  // inactive rows: t < first or t >= last
-  const int t1 = min(t0 + kFillRows, a.T);
-  if (t0 >= first && t1 <= last) return;
-  const int chunks = a.row_bytes / 4;  // row_bytes is a multiple of 4
-  for (int i = threadIdx.x; i < kFillRows * a.H * chunks; i += kThreads) {
-    const int tt = i / (a.H * chunks);
-    const int rem = i % (a.H * chunks);
-    const int h = rem / chunks, c = rem % chunks;
-    const int t = t0 + tt;
-    if (t >= a.T || (t >= first && t < last)) continue;
-    char* row = (char*)a.x + ((int64_t)t * a.st + (int64_t)h * a.sh) * a.elem_bytes;
-    ((uint32_t*)row)[c] = 0u;
-    if (c == 0 && a.lse != nullptr) a.lse[(int64_t)h * a.lse_sh + t] = -INFINITY;
+  last = last < first ? first : (last > a.T ? a.T : last);
+  const int n_pad = first + (a.T - last);  // padding row j: j < first ? j : last + (j - first)
+  const int chunks = a.row_bytes / 4;      // row_bytes is a multiple of 4
+  for (int j0 = b * kFillRows; j0 < n_pad; j0 += fill_blocks * kFillRows) {
+    for (int i = threadIdx.x; i < kFillRows * a.H * chunks; i += kThreads) {
+      const int tt = i / (a.H * chunks);
+      const int rem = i % (a.H * chunks);
+      const int h = rem / chunks, c = rem % chunks;
+      const int j = j0 + tt;
+      if (j >= n_pad) continue;
+      const int t = j < first ? j : last + (j - first);
+      char* row = (char*)a.x + ((int64_t)t * a.st + (int64_t)h * a.sh) * a.elem_bytes;
+      ((uint32_t*)row)[c] = 0u;
+      if (c == 0 && a.lse != nullptr) a.lse[(int64_t)h * a.lse_sh + t] = -INFINITY;
+    }
   }
 }
 
@@ -494,7 +501,7 @@ __global__ __launch_bounds__(kThreads) void prologue_kernel(const PrologueArgs a
     b -= a.delta_blocks;
   }
   const int target = b / a.fill_blocks;
-  fill_block(a.fill[target], b - target * a.fill_blocks);
+  fill_block(a.fill[target], b - target * a.fill_blocks, a.fill_blocks);
 }
 
 }  // namespace
@@ -629,7 +636,9 @@ hipError_t launch_prologue(const Prologue& pro, hipStream_t stream) {
   for (int i = 0; i < pro.nfill; ++i)
     if (pro.fill[i].T > 0 && pro.fill[i].H > 0) {
       a.fill[a.nfill++] = pro.fill[i];
-      a.fill_blocks = (pro.fill[i].T + kFillRows - 1) / kFillRows;  // every target has the same T
+      // every target has the same T; at most kFillWgs workgroups each
+      const int rows = (pro.fill[i].T + kFillRows - 1) / kFillRows;
+      a.fill_blocks = rows < kFillWgs ? rows : kFillWgs;
     }
   const int64_t blocks = (int64_t)a.nplan + a.delta_blocks + a.kscan_blocks + (int64_t)a.nfill * a.fill_blocks;
   if (blocks == 0) return hipSuccess;
