@@ -171,11 +171,13 @@ def test_padded_small_grid_is_cut(device, key_chunks):
     assert errs[0] <= 2e-2 and errs[1] <= 1e-2
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("split", [_capi.SPLIT_ALWAYS, _capi.SPLIT_NEVER], ids=["split", "plain"])
-def test_chunked_forward_gate_rope(device, split, key_chunks):
+def test_chunked_forward_gate_rope(device, split, d, key_chunks):
     """Gated output, RoPE of q in the kernel (with the rotated q written out) and the P hi + lo
-    split all ride on the merged accumulator: chunked and uncut agree as above."""
-    case = make_case([3500, 800], [2000, 0], 2, 2, 128, seed=47, dtype=torch.bfloat16)
+    split all ride on the merged accumulator: chunked and uncut agree as above (both head dims,
+    so that the gated split bodies of both run)."""
+    case = make_case([3500, 800], [2000, 0], 2, 2, d, seed=47, dtype=torch.bfloat16)
     c = case.to(device)
     T, hq, d = c.q.shape
     g = torch.Generator().manual_seed(48)

@@ -155,16 +155,18 @@ def test_long_context_full_fp64_reference(device):
         torch.testing.assert_close(dq_r[rows, h].cpu(), ds @ kh, rtol=1e-9, atol=1e-9)
 
 
-def test_split_decision_on_the_device(device):
+@pytest.mark.parametrize("d", [128, 64])
+def test_split_decision_on_the_device(device, d):
     """AUTO splits P and dS exactly when softmax_scale * max|K| > 0.75: bitwise ALWAYS on an
     outlier input and bitwise NEVER on a plain one (so the decision is what changes the
-    result), and on the outlier input the split brings dQ within the bar of the fp64 closed
-    form (5e-2, or two bf16 half-ulps of a channel's max|ref| above it), which the unsplit
-    kernels miss."""
+    result), and on the outlier input the split brings O, dQ, dK and dV within the bar of the
+    fp64 closed form (5e-2, or two bf16 half-ulps of a channel's max|ref| above it), which the
+    unsplit kernels miss for dQ.  Both head dims, so that the split bodies of both kernel
+    families run."""
     mode = P._split_mode
     try:
         for outlier, same in ((20.0, "always"), (None, "never")):
-            case = make_case([1500, 700], [600, 0], 8, 2, 128, seed=31, dtype=torch.bfloat16, outlier=outlier)
+            case = make_case([1500, 700], [600, 0], 8, 2, d, seed=31, dtype=torch.bfloat16, outlier=outlier)
             res = {}
             for m in ("auto", "always", "never"):
                 P.set_split_mode(m)
@@ -177,7 +179,7 @@ def test_split_decision_on_the_device(device):
                 for i, name in ((0, "O"), (2, "dQ"), (3, "dK"), (4, "dV")):
                     r_split = channel_excess(res["always"][i], ref[i]).max().item()
                     r_plain = channel_excess(res["never"][i], ref[i]).max().item()
-                    print(f"[split] outlier {name}: error / bound split {r_split:.3g}, unsplit {r_plain:.3g}",
+                    print(f"[split] d {d} outlier {name}: error / bound split {r_split:.3g}, unsplit {r_plain:.3g}",
                           flush=True)
                     assert r_split <= 1, (name, r_split)
                 assert channel_excess(res["never"][2], ref[2]).max().item() > 1  # dQ needs the split
