@@ -78,7 +78,6 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a) {
   const int rank = blockIdx.x / a.Hkv;
   const int hk = blockIdx.x - rank * a.Hkv;
   const int4 item = a.plan_k[rank];  // never split for this kernel: part 0
-  if (split_on(a, lane) != kSplit) return;
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int ktile = item.y;

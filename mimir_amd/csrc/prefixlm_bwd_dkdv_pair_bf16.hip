@@ -91,8 +91,8 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a, uint64_t seg) {
   const Loader ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane), ldv(a.v_st, wave, lane);
   const TileLanes<D> tl(lane);
   const float c2 = a.scale_log2;
-  // kSplit: dS as bf16 hi + lo in the dK product (the kernels pick the body).
-  if (split_on(a, lane) != kSplit) return;
+  // kSplit: dS as bf16 hi + lo in the dK product (the kernels pick the body by
+  // the split decision).
   auto fetch_unit = [&]() {  // next work unit from the launch-wide queue
     return (int)gridDim.x + __hip_atomic_fetch_add(&a.queue[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };

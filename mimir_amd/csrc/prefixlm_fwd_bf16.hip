@@ -106,12 +106,11 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, uint64_t seg) {
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
-  // P as bf16 hi + lo in the P V product (wave-uniform): O, and the backward's
-  // delta = rowsum(dO * O), then carry no rounding of P.  Workgroup 0 records
-  // the decision before anything can end it early.
-  const bool split_call = split_decision(a.split_mode, a.kscan, nullptr, lane);
-  if (a.split_flag != nullptr && blockIdx.x == 0 && tid == 0) *a.split_flag = split_call ? 1 : 0;
-  if (split_call != (kSplit == 1)) return;
+  // P as bf16 hi + lo in the P V product (the kernel picked this body by the
+  // split decision): O, and the backward's delta = rowsum(dO * O), then carry no
+  // rounding of P.  Workgroup 0 records the decision before anything can end it
+  // early.
+  if (a.split_flag != nullptr && blockIdx.x == 0 && tid == 0) *a.split_flag = kSplit;
   constexpr bool split = kSplit == 1;
 
   // Workgroup -> (list entry, head), see the grid in launch(): unit = entry *
