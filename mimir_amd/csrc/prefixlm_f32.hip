@@ -3,8 +3,8 @@
 // The fp32 path serves the reference's CPU training precision
 // (flash_attention_prefixlm_dense.py runs in fp32) and is held to the fp32
 // oracle at 1e-5, so it keeps every product and sum in fp32 on the vector ALUs:
-// four lanes share one row (D/4 contiguous values each) and combine dot products
-// with two cross-lane adds.  K/V (forward, dQ) or Q/dO (dK/dV) tiles are staged in
+// four lanes share one row (D/4 contiguous values each; eight in the forward) and
+// combine dot products with cross-lane adds.  K/V (forward, dQ) or Q/dO (dK/dV) tiles are staged in
 // LDS and read as broadcasts.  Structure and ownership follow the Metal kernels
 // of flash_attention_prefixlm_mps.py (forward 391-476, dQ 967-1039, dK/dV
 // 1245-1322), extended to GQA.
@@ -80,26 +80,41 @@ __device__ __forceinline__ float dot_tile(const float (&x)[D / 4], const float* 
   return sum4(acc);
 }
 
+// The forward gives each row eight lanes (D / 8 values each; the dot products
+// combine with three cross-lane adds), so 32 rows per workgroup: twice the
+// workgroups, and waves, of four lanes per row on the same batch, which the
+// tile loop's LDS broadcast reads need to hide their latency.
+constexpr int kFwdLanes = 8;
+constexpr int kFwdRows = kThreads / kFwdLanes;
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
-  constexpr int EPL = D / 4;
+  constexpr int EPL = D / kFwdLanes;
+  static_assert(EPL % 4 == 0, "whole float4 per lane");
   __shared__ __attribute__((aligned(16))) float sK[kTile * D];
   __shared__ __attribute__((aligned(16))) float sV[kTile * D];
   const int h = blockIdx.x % a.Hq;
   const int s = blockIdx.x / a.Hq;
   const int tile = a.num_tiles - 1 - (int)blockIdx.y;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
-  const int m0 = tile * kRowsPerBlock;
+  const int m0 = tile * kFwdRows;
   if (m0 >= g.nq) return;
   const int hk = h / a.group;
-  const int sub = threadIdx.x & 3;
-  const int qpos = m0 + (threadIdx.x >> 2);
+  const int sub = threadIdx.x % kFwdLanes;
+  const int qpos = m0 + threadIdx.x / kFwdLanes;
   const bool valid = qpos < g.nq;
   const int kend = kend_of(g.p, qpos);
-  const int wg_kend = max(g.p, min(m0 + kRowsPerBlock, g.nq));
+  const int wg_kend = max(g.p, min(m0 + kFwdRows, g.nq));
 
   float qv[EPL], acc[EPL];
-  load_row<D>(qv, a.q + (int64_t)(g.start + qpos) * a.q_st + (int64_t)h * a.q_sh, sub, valid);
+  {
+    const float* qrow = a.q + (int64_t)(g.start + qpos) * a.q_st + (int64_t)h * a.q_sh + sub * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; e += 4) {
+      const f32x4 t = valid ? *(const f32x4*)&qrow[e] : f32x4{0.f, 0.f, 0.f, 0.f};
+      qv[e] = t[0]; qv[e + 1] = t[1]; qv[e + 2] = t[2]; qv[e + 3] = t[3];
+    }
+  }
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
@@ -115,7 +130,18 @@ __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < kTile; ++j) {
-      float x = dot_tile<D>(qv, &sK[j * D], sub);
+      float x = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; e += 4) {
+        const f32x4 t = *(const f32x4*)&sK[j * D + sub * EPL + e];
+        x = __builtin_fmaf(qv[e], t[0], x);
+        x = __builtin_fmaf(qv[e + 1], t[1], x);
+        x = __builtin_fmaf(qv[e + 2], t[2], x);
+        x = __builtin_fmaf(qv[e + 3], t[3], x);
+      }
+      x += __shfl_xor(x, 1, 64);
+      x += __shfl_xor(x, 2, 64);
+      x += __shfl_xor(x, 4, 64);
       if (k0 + j >= kend) x = -INFINITY;
       sc[j] = x;
       mx = fmaxf(mx, x);
@@ -327,7 +353,7 @@ hipError_t launch_fwd(const MimirPrefixLMFwdParams& p, hipStream_t stream) {
   a.v_st = p.v_stride_token; a.v_sh = p.v_stride_head;
   a.o_st = p.out_stride_token; a.o_sh = p.out_stride_head;
   a.lse_sh = p.lse_stride_head;
-  a.num_tiles = (p.max_seqlen_all + kRowsPerBlock - 1) / kRowsPerBlock;
+  a.num_tiles = (p.max_seqlen_all + kFwdRows - 1) / kFwdRows;
   if (a.num_tiles == 0 || p.numseqs == 0) return hipSuccess;
   hipLaunchKernelGGL(fwd_f32_kernel<D>, dim3(p.num_q_heads * p.numseqs, a.num_tiles), dim3(kThreads), 0,
                      stream, a);
