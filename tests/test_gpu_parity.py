@@ -129,6 +129,24 @@ def test_bf16_random_shapes(device, seed):
     check(case, device, label=f"random{seed} hq={hq} hkv={hkv} d={d} causal={causal} pad={pad_to}")
 
 
+@pytest.mark.parametrize("seed", range(16, 24))
+def test_bf16_random_shapes_split(device, seed):
+    """Further seeded random shapes with split mode "always": the split bodies (P and dS as two
+    bf16 halves) of the forward and of both dK/dV kernels over the same kind of packings,
+    against the same bars."""
+    from mimir_amd import prefixlm as P
+
+    seq_lens, prefixes, hq, hkv, d, pad_to, causal = _random_shape(seed)
+    case = make_case(seq_lens, prefixes, hq, hkv, d, seed=seed, dtype=torch.bfloat16, pad_to=pad_to,
+                     is_causal=causal)
+    mode = P._split_mode
+    try:
+        P.set_split_mode("always")
+        check(case, device, label=f"random-split{seed} hq={hq} hkv={hkv} d={d} causal={causal} pad={pad_to}")
+    finally:
+        P._split_mode = mode
+
+
 @pytest.fixture
 def dscore_limit():
     """Set the score-gradient workspace limit for one test; the default comes back after."""
