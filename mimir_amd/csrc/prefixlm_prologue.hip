@@ -412,40 +412,64 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
 
 // K magnitude scan: workgroup b sets slot b to 1 if a bf16 element of its share
 // of the key rows inside sequences, tokens [cu_seqlens[0], cu_seqlens[numseqs])
-// of the [T, Hkv, D] rows (16-byte units b * 256 + threadIdx.x, then every
-// kKScanSlots * 256 units), has |k| > the threshold, else to 0.  Padding rows
+// of the [T, Hkv, D] rows, has |k| > the threshold, else to 0.  The
+// kKScanSlots * 256 threads take the Hkv * D / 8 sixteen-byte units of a row
+// side by side (consecutive threads, consecutive units of a head) and step
+// down the rows: the address arithmetic is additions, not a division per
+// unit, which bounded the scan by the VALU rather than by HBM.  Padding rows
 // are never attended, so whatever they hold cannot change the decision.
 // Magnitudes are compared as integers: for finite bf16 the bits with the sign
 // cleared order like the values (a NaN compares above any threshold and sets
 // the slot).
 __device__ void kscan_block(const KScanArgs& a, int b) {
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-  const int upr = a.D / 8;  // 16-byte units per row
+  const int upr = a.D / 8;  // 16-byte units per row and head
   int first = a.numseqs > 0 ? a.cu_seqlens[0] : 0;
   int last = a.numseqs > 0 ? a.cu_seqlens[a.numseqs] : 0;
   first = first < 0 ? 0 : (first > a.T ? a.T : first);
   last = last < first ? first : (last > a.T ? a.T : last);
-  const int64_t units = (int64_t)(last - first) * a.Hkv * upr;
-  const int64_t step = (int64_t)kKScanSlots * kThreads;
+  const int rows = last - first;
+  const int row_units = a.Hkv * upr;  // units of one packed row, all kv heads
+  constexpr int kScanThreads = kKScanSlots * kThreads;
   u16x2 mx = {0, 0};
-  for (int64_t u0 = (int64_t)b * kThreads + threadIdx.x; u0 < units; u0 += 4 * step) {
-    i32x4 w[4];
+  auto fold = [&](i32x4 w) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {  // all four loads issued before the first use
-      const int64_t u = u0 + j * step;
-      w[j] = i32x4{0, 0, 0, 0};
-      if (u < units) {
-        const int64_t row = u / upr;
-        const int c = (int)(u - row * upr);
-        const int r = (int)(row / a.Hkv), hk = (int)(row - (int64_t)r * a.Hkv);
-        w[j] = *(const i32x4*)&a.k[(int64_t)(first + r) * a.k_st + (int64_t)hk * a.k_sh + c * 8];
+    for (int e = 0; e < 4; ++e) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2, w[e] & 0x7fff7fff));
+  };
+  const int t = b * kThreads + threadIdx.x;
+  if (row_units <= kScanThreads) {
+    // Thread t keeps one unit (kv head, column) of every row_step-th row from
+    // row t / row_units on: one division per thread, then additions only.
+    const int row_step = kScanThreads / row_units;
+    const int r0 = t / row_units;
+    if (r0 < row_step) {
+      const int cu = t - r0 * row_units;
+      const int hk = cu / upr, c = cu - hk * upr;
+      const bf16_t* p = a.k + (int64_t)(first + r0) * a.k_st + (int64_t)hk * a.k_sh + c * 8;
+      const int64_t pstep = (int64_t)row_step * a.k_st;
+      int64_t r = r0;
+      for (; r + 3 * row_step < rows; r += 4 * row_step) {  // four loads in flight
+        i32x4 w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = *(const i32x4*)(p + j * pstep);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fold(w[j]);
+        p += 4 * pstep;
+      }
+      for (; r < rows; r += row_step) {
+        fold(*(const i32x4*)p);
+        p += pstep;
       }
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2, w[j][e] & 0x7fff7fff));
+  } else {
+    // Rows wider than the grid (Hkv * D > 8 * kScanThreads): unit by unit.
+    const int64_t units = (int64_t)rows * row_units;
+    for (int64_t u = t; u < units; u += kScanThreads) {
+      const int64_t row = u / row_units;
+      const int cu = (int)(u - row * row_units);
+      const int hk = cu / upr, c = cu - hk * upr;
+      fold(*(const i32x4*)&a.k[(int64_t)(first + row) * a.k_st + (int64_t)hk * a.k_sh + c * 8]);
+    }
   }
   const int over = (uint32_t)mx[0] > a.thr_bits || (uint32_t)mx[1] > a.thr_bits;
   const int any = __syncthreads_or(over);

@@ -29,12 +29,14 @@ Invariants (every bf16 workload):
   active queries of dO, summed over the q-heads of each kv head (rows of P sum to 1).
 """
 
+import ctypes
 import dataclasses
 import math
 
 import pytest
 import torch
 
+from mimir_amd import _capi
 from mimir_amd import prefixlm as P
 from mimir_amd import prefixlm_attn_fwd
 from mimir_amd.workloads import make_case, make_config
@@ -209,3 +211,47 @@ def test_split_decision_ignores_padding_keys(device):
                 assert torch.equal(a, b), fill
     finally:
         P._split_mode = mode
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hkv,d,wide", [(1, 128, False), (3, 64, False), (4, 128, True), (2, 64, True)])
+def test_k_scan_reaches_every_key(device, hkv, d, wide):
+    """The K scan behind AUTO reads every element of every key row inside the sequences: one
+    element with softmax_scale * |k| = 1.125 (threshold 0.75), planted at the first or last
+    real row, the first or last column, each kv head, or at random, turns the recorded decision
+    to split; the same input without it, or with it in a padding row, does not.  With `wide`, K
+    is a strided view (token stride (Hkv + 3) * D, as a slice of the gqkv projection)."""
+    lib = _capi.load()
+    case = make_case([700, 1, 333], [100, 1, 0], 2 * hkv, hkv, d, seed=40 + hkv, dtype=torch.bfloat16,
+                     pad_to=1100)
+    c = case.to(device)
+    T, real = c.k.shape[0], sum(case.seq_lens)
+    scale = d ** -0.5
+    base = (c.k.float() * 0.25).to(torch.bfloat16)  # max |k| ~ 1.3: scale * max|k| < 0.2
+    gen = torch.Generator().manual_seed(hkv * 1000 + d)
+
+    def decision(k):
+        if wide:
+            big = torch.zeros(T, hkv + 3, d, dtype=torch.bfloat16, device=device)
+            big[:, 1:1 + hkv] = k
+            k = big[:, 1:1 + hkv]
+        flag = torch.full((1,), -1, dtype=torch.int32, device=device)
+        p, out, lse, keep = P.prepare_fwd(c.q, k, c.v, False, c.prefix_lens, c.causal_lens, c.cu_seqlens,
+                                          c.total_seqlen, c.numseqs, c.max_seqlen_all, scale,
+                                          split_mode=_capi.SPLIT_AUTO, split_flag=flag)
+        _capi.raise_for_status(lib, lib.mimir_prefixlm_fwd(ctypes.byref(p), torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        return int(flag.item())
+
+    assert decision(base) == 0
+    spots = [(0, 0, 0), (real - 1, hkv - 1, d - 1), (real - 1, 0, 0), (0, hkv - 1, d - 1)]
+    spots += [(int(torch.randint(0, real, (1,), generator=gen)), h, int(torch.randint(0, d, (1,), generator=gen)))
+              for h in range(hkv) for _ in range(3)]
+    for row, h, col in spots:
+        for sign in (1.0, -1.0):
+            k = base.clone()
+            k[row, h, col] = sign * 1.125 / scale
+            assert decision(k) == 1, (row, h, col, sign)
+    k = base.clone()
+    k[real:, :, :] = 1.125 / scale  # padding rows only
+    assert decision(k) == 0
