@@ -357,6 +357,7 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
   constexpr int RPP = kThreads / LPR;   // rows per pass
   const int c = threadIdx.x % LPR;
   const int64_t rows = (int64_t)a.T * a.Hq;
+  const bool rows32 = rows <= 0x7fffffff;  // (token, head) of a row by a 32-bit division
   bf16x8 ov[kDeltaPasses], dv[kDeltaPasses], gv[kDeltaPasses], lv[kDeltaPasses];
   int t[kDeltaPasses], h[kDeltaPasses];
   bool valid[kDeltaPasses];
@@ -365,7 +366,7 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
   for (int i = 0; i < kDeltaPasses; ++i) {
     const int64_t row = ((int64_t)b * kDeltaPasses + i) * RPP + threadIdx.x / LPR;  // row = t * Hq + h
     valid[i] = row < rows;
-    t[i] = valid[i] ? (int)(row / a.Hq) : 0;
+    t[i] = !valid[i] ? 0 : rows32 ? (int)((uint32_t)row / (uint32_t)a.Hq) : (int)(row / a.Hq);
     h[i] = valid[i] ? (int)(row - (int64_t)t[i] * a.Hq) : 0;
     if (valid[i]) {
       ov[i] = *(const bf16x8*)&a.o[(int64_t)t[i] * a.o_st + (int64_t)h[i] * a.o_sh + c * 8];
