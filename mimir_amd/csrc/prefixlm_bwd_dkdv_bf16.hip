@@ -102,7 +102,7 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a) {
   // Iteration it covers q head hk * G + it / nqt and query tile it % nqt.  The
   // tile copies walk that order with running addresses (adds only, no division
   // per tile).
-  const TileLoader<D, kDkWaves> ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane);
+  const TileLoader<D, kDkWaves, true> ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane);
   const uint32_t q_st32 = (uint32_t)a.q_st, o_st32 = (uint32_t)a.do_st;
   const int qh0 = hk * a.group;
   const bf16_t* q_head = a.q + ((int64_t)g.start + q_begin) * a.q_st + (int64_t)qh0 * a.q_sh;
@@ -153,8 +153,9 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a) {
     vf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rv, (uint32_t)((key * a.v_st + 16 * ks + 8 * hi) * 2)));
   }
   issue_next(n_iter > 1, sQ1, sO1, sL1);
-  // Buffer loads per issue() and wave: Q and dO tiles plus one lse2 / delta row.
-  constexpr int kLoadsPerIssue = 2 * TileLoader<D, kDkWaves>::kPerWave + 1;
+  // Buffer loads per issue() and wave: Q and dO tiles plus one lse2 / delta row
+  // (every wave issues kPerWave copies per tile: the loaders repeat the last).
+  constexpr int kLoadsPerIssue = 2 * TileLoader<D, kDkWaves, true>::kPerWave + 1;
   // Tile `it` has landed everywhere; the copies of tile it + 1 may still be in flight.
   auto sync_stage = [&]() { stage_barrier<kLoadsPerIssue>(); };
 

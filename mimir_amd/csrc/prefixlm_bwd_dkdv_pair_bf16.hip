@@ -191,10 +191,15 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a, uint64_t seg) {
     kf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
   }
   issue_next(n_iter > 1, sQ1, sO1, sL1);
-  constexpr int kLoadsPerIssue = 2 * Loader::kPerWave + 1;
+  constexpr int kLoadsPerIssue = 2 * Loader::kPerWave + 1;  // with the last round's copies
   // Tile `it` has landed everywhere; the copies of tile it + 1 (and dS stores
   // after them) may still be in flight.
-  auto sync_stage = [&]() { stage_barrier<kLoadsPerIssue>(); };
+  auto sync_stage = [&]() {
+    if (ldq.has_last)
+      stage_barrier<kLoadsPerIssue>();
+    else
+      stage_barrier<kLoadsPerIssue - 2>();
+  };
 
   f32x16 dkacc[DT], dvacc[DT];
 #pragma unroll

@@ -331,10 +331,16 @@ struct TileLayout {
 // rebuilds the (scalar) buffer resource, whose base is the tile's first row and
 // whose size covers the rows still inside the sequence -- rows beyond it read as
 // zeros.  The kRowUnits wave instructions of a tile are spread over the NWAVES
-// waves; a wave left without one of its own repeats the last instruction (the
-// same data to the same place).  Completion is tracked by vmcnt; callers wait
-// before the barrier that publishes the tile.
-template <int D, int NWAVES>
+// waves, each issued once: kPerWave per wave, or one fewer for the waves
+// without a share of the last round (`has_last` false).  With kRepeatLast such
+// a wave repeats the last instruction instead (the same data to the same
+// place), which keeps the count uniform: 7 extra copies per 17 in the 8-wave
+// dK / dV kernel, which made it and the forward ~1-2% slower, but 2% faster for
+// the head_dim 64 dK / dV kernel (9 copies on 4 waves), which keeps it.
+// Completion is tracked by vmcnt; callers wait before the barrier that
+// publishes the tile, counting kPerWave or kPerWave - 1 copies per tile by
+// `has_last`.
+template <int D, int NWAVES, bool kRepeatLast = false>
 struct TileLoader {
   using L = TileLayout<D>;
   static constexpr int kInst = L::kRowUnits;  // 64 rows * kRowUnits units / 64 lanes
@@ -342,8 +348,10 @@ struct TileLoader {
   uint32_t voff[kPerWave];
   int lds[kPerWave];  // element offset of each instruction's 1 KiB (wave-uniform)
   int64_t st;
+  bool has_last;  // this wave issues an instruction of the last round (wave-uniform; always with kRepeatLast)
 
   __device__ __forceinline__ TileLoader(int64_t stride, int wave, int lane) : st(stride) {
+    has_last = kRepeatLast || (kPerWave - 1) * NWAVES + wave < kInst;
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) {
       const int g = min(i * NWAVES + wave, kInst - 1);
@@ -363,9 +371,11 @@ struct TileLoader {
   __device__ __forceinline__ void issue_at(const bf16_t* first_row, uint32_t bytes, bf16_t* tile) const {
     const __amdgpu_buffer_rsrc_t r = make_rsrc(first_row, bytes);
 #pragma unroll
-    for (int i = 0; i < kPerWave; ++i)
+    for (int i = 0; i < kPerWave; ++i) {
+      if (i == kPerWave - 1 && !has_last) break;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(tile + lds[i]), 16,
                                                voff[i], 0, 0, 0);
+    }
   }
 };
 
