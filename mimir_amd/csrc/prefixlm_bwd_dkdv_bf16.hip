@@ -102,13 +102,19 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a) {
   // Iteration it covers q head hk * G + it / nqt and query tile it % nqt.  The
   // tile copies walk that order with running addresses (adds only, no division
   // per tile).
-  const TileLoader<D, kDkWaves, true> ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane);
+  // Every wave issues the same number of copies per tile: the Q tile's last
+  // instruction is wave 0's, the dO tile's wave 1's (rotated loader), and the
+  // other waves load the lse2 row (wave 2) and the delta row (the rest).
+  using Loader = TileLoader<D, kDkWaves>;
+  static_assert(Loader::kInst == (Loader::kPerWave - 1) * kDkWaves + 1 && kDkWaves >= 4,
+                "one last-round copy per tile, on waves 0 / 1; rows on waves 2 and up");
+  const Loader ldq(a.q_st, wave, lane), ldo(a.do_st, wave, lane, 1);
   const uint32_t q_st32 = (uint32_t)a.q_st, o_st32 = (uint32_t)a.do_st;
   const int qh0 = hk * a.group;
   const bf16_t* q_head = a.q + ((int64_t)g.start + q_begin) * a.q_st + (int64_t)qh0 * a.q_sh;
   const bf16_t* o_head = a.dout + ((int64_t)g.start + q_begin) * a.do_st + (int64_t)qh0 * a.do_sh;
-  // one 4-byte row per wave: wave 0 lse2, the others delta (same data to the same place)
-  const float* r_head = (wave == 0 ? a.lse2 : a.delta) + (int64_t)qh0 * a.T + g.start + q_begin;
+  // one 4-byte row per wave from wave 2 on: wave 2 lse2, the others delta (same data to the same place)
+  const float* r_head = (wave == 2 ? a.lse2 : a.delta) + (int64_t)qh0 * a.T + g.start + q_begin;
   const bf16_t* i_q = q_head;
   const bf16_t* i_o = o_head;
   const float* i_r = r_head;
@@ -123,8 +129,9 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a) {
     ldq.issue_at(i_q, rows_bytes32(rows, q_st32, D), tq);
     ldo.issue_at(i_o, rows_bytes32(rows, o_st32, D), to);
     const __amdgpu_buffer_rsrc_t r = make_rsrc(i_r, rows > 0 ? (uint32_t)rows * 4u : 0u);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(tl + (wave == 0 ? 0 : kBwdBlockQT)),
-                                             4, (uint32_t)lane * 4u, 0, 0, 0);
+    if (wave >= 2)  // waves 0 / 1 issue the tiles' last copy instead
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(tl + (wave == 2 ? 0 : kBwdBlockQT)),
+                                               4, (uint32_t)lane * 4u, 0, 0, 0);
     if (++i_qt == nqt) {
       i_qt = 0;
       i_rows = g.nq - q_begin;
@@ -153,9 +160,9 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a) {
     vf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rv, (uint32_t)((key * a.v_st + 16 * ks + 8 * hi) * 2)));
   }
   issue_next(n_iter > 1, sQ1, sO1, sL1);
-  // Buffer loads per issue() and wave: Q and dO tiles plus one lse2 / delta row
-  // (every wave issues kPerWave copies per tile: the loaders repeat the last).
-  constexpr int kLoadsPerIssue = 2 * TileLoader<D, kDkWaves, true>::kPerWave + 1;
+  // Buffer loads per issue() and wave: 2 * kPerWave - 1 on every wave (Q and dO
+  // tiles with the last copy of one of them, or both without it and a row).
+  constexpr int kLoadsPerIssue = 2 * Loader::kPerWave - 1;
   // Tile `it` has landed everywhere; the copies of tile it + 1 may still be in flight.
   auto sync_stage = [&]() { stage_barrier<kLoadsPerIssue>(); };
 

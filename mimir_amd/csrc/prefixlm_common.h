@@ -332,15 +332,14 @@ struct TileLayout {
 // whose size covers the rows still inside the sequence -- rows beyond it read as
 // zeros.  The kRowUnits wave instructions of a tile are spread over the NWAVES
 // waves, each issued once: kPerWave per wave, or one fewer for the waves
-// without a share of the last round (`has_last` false).  With kRepeatLast such
-// a wave repeats the last instruction instead (the same data to the same
-// place), which keeps the count uniform: 7 extra copies per 17 in the 8-wave
-// dK / dV kernel, which made it and the forward ~1-2% slower, but 2% faster for
-// the head_dim 64 dK / dV kernel (9 copies on 4 waves), which keeps it.
-// Completion is tracked by vmcnt; callers wait before the barrier that
-// publishes the tile, counting kPerWave or kPerWave - 1 copies per tile by
-// `has_last`.
-template <int D, int NWAVES, bool kRepeatLast = false>
+// without a share of the last round (`has_last` false); `rot` picks which
+// waves share it, so that two loaders can give their last instructions to
+// different waves.  (Repeating the last instruction on the other waves, the
+// same data to the same place, kept every wave's count uniform at the cost of
+// 7 extra copies per 17 in an 8-wave workgroup: the forward and dK / dV ran
+// ~1-2% slower.)  Completion is tracked by vmcnt; callers wait before the
+// barrier that publishes the tile, counting each wave's own copies.
+template <int D, int NWAVES>
 struct TileLoader {
   using L = TileLayout<D>;
   static constexpr int kInst = L::kRowUnits;  // 64 rows * kRowUnits units / 64 lanes
@@ -348,13 +347,15 @@ struct TileLoader {
   uint32_t voff[kPerWave];
   int lds[kPerWave];  // element offset of each instruction's 1 KiB (wave-uniform)
   int64_t st;
-  bool has_last;  // this wave issues an instruction of the last round (wave-uniform; always with kRepeatLast)
+  bool has_last;  // this wave issues an instruction of the last round (wave-uniform)
 
-  __device__ __forceinline__ TileLoader(int64_t stride, int wave, int lane) : st(stride) {
-    has_last = kRepeatLast || (kPerWave - 1) * NWAVES + wave < kInst;
+  // Wave (rot + j) % NWAVES issues instructions j, j + NWAVES, j + 2 NWAVES, ...
+  __device__ __forceinline__ TileLoader(int64_t stride, int wave, int lane, int rot = 0) : st(stride) {
+    const int wr = (wave + NWAVES - rot) % NWAVES;
+    has_last = (kPerWave - 1) * NWAVES + wr < kInst;
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) {
-      const int g = min(i * NWAVES + wave, kInst - 1);
+      const int g = min(i * NWAVES + wr, kInst - 1);
       const int u = g * 64 + lane;
       const int prow = u / L::kRowUnits;
       const int c = u - prow * L::kRowUnits;
