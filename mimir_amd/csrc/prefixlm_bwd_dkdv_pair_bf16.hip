@@ -191,7 +191,12 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a, uint64_t seg) {
     kf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((key * a.k_st + 16 * ks + 8 * hi) * 2)));
   }
   issue_next(n_iter > 1, sQ1, sO1, sL1);
-  constexpr int kLoadsPerIssue = 2 * Loader::kPerWave + 1;  // with the last round's copies
+  // Copies per issue_next and wave: the Q and dO loaders share one assignment,
+  // so a wave with the last round's instructions (wave 0) issues 2 * kPerWave + 1
+  // with its lse2 / delta row, the others two fewer.  (Giving the dO tile's last
+  // instruction to wave 1 instead, as the head_dim 64 kernel does, made the
+  // compiler fail on the split body here.)
+  constexpr int kLoadsPerIssue = 2 * Loader::kPerWave + 1;
   // Tile `it` has landed everywhere; the copies of tile it + 1 (and dS stores
   // after them) may still be in flight.
   auto sync_stage = [&]() {
