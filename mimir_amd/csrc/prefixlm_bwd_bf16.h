@@ -47,7 +47,6 @@ struct BwdArgs {
   const int* kscan;  // workspace: the DELTA stage's K magnitude slots (kKScanSlots)
   const int* split_flag;  // the forward's recorded split decision, or NULL
   int split_mode;    // MimirSplitMode
-  int dq_companion;  // 1: the recomputing dQ kernel enqueued beside the hand-off's
   RopeTab rope;      // optional: dQ / dK stored as gradients of the unrotated q / k
 };
 

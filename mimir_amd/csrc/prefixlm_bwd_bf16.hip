@@ -93,7 +93,6 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
   a.kscan = (const int*)(wsb + ws.kscan);
   a.split_flag = p.split_flag;
   a.split_mode = p.split_mode;
-  a.dq_companion = 0;
   a.rope = RopeTab{p.rope_cos, p.rope_sin, p.rope_stride_token};
 
   if (stages & MIMIR_BWD_STAGE_DELTA) {

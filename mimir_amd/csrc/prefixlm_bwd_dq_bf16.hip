@@ -14,11 +14,11 @@ constexpr int kBlockK = 64;   // keys per LDS tile
 // dQ.  Mirrors the forward's S^T formulation: each lane owns one query column,
 // so lse and delta are lane-local and dS^T feeds the B operand of dQ^T += K^T dS^T
 // directly; K^T fragments come from the row-major K tile via ds_read_b64_tr_b16.
-// Workgroup r * Hq + h takes head h of entry r of the query-tile work list
+// Workgroup b = r * Hq + h takes head h of entry r of the query-tile work list
 // (prefixlm_prologue.hip): longest key ranges first.
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
+__device__ __forceinline__ void dq_tiles(const BwdArgs& a, int b) {
   constexpr int DT = D / 32;
   constexpr int KS = D / 16;
   using L = TileLayout<D>;
@@ -33,8 +33,8 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-  const int rank = blockIdx.x / a.Hq;
-  const int h = blockIdx.x - rank * a.Hq;
+  const int rank = b / a.Hq;
+  const int h = b - rank * a.Hq;
   const int4 item = a.plan[rank];
   if (item.x < 0) return;  // list padding
   const int s = item.x;
@@ -44,10 +44,8 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
   const int m0 = qtile * kBlockQ;
   if (m0 >= g.nq) return;
   const int hk = h / a.group;
-  // dS split into bf16 hi + lo for the dQ product (wave-uniform); beside the
-  // score-gradient hand-off this kernel works only when the hand-off cannot.
+  // dS split into bf16 hi + lo for the dQ product (wave-uniform)
   const bool split = split_on(a, lane);
-  if (a.dq_companion && !dq_needs_recompute(a, split)) return;
 
   const int wg_kend = max(g.p, min(m0 + kBlockQ, g.nq));
   const int nkt_all = (wg_kend + kBlockK - 1) / kBlockK;
@@ -216,11 +214,45 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
 }
 
 template <int D>
+__global__ __launch_bounds__(kThreads, 2) void dq_kernel(const BwdArgs a) {
+  dq_tiles<D>(a, blockIdx.x);
+}
+
+// The launch beside the score-gradient hand-off's dQ (head_dim 128), which works
+// only when the hand-off cannot (dS split, or a tile that did not fit the
+// region).  It checks that first, so that when it has nothing to do its
+// workgroups exit after one round of loads instead of three dependent ones (list
+// entry, sequence, flags).  (A grid of one resident round looping over the
+// entries would exit sooner still, but the loop spills ~50 registers in the
+// work it does when the hand-off is ruled out.)
+__global__ __launch_bounds__(kThreads, 2) void dq_companion_kernel(const BwdArgs a) {
+  // The flags are read with atomic loads, which are not merged with the body's
+  // reads of them: a decision kept live across the body cost it a register spill.
+  auto flag = [](const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  bool work = a.split_mode == MIMIR_SPLIT_ALWAYS || flag(&a.queue[kDsIncomplete]) != 0;
+  if (!work && a.split_mode == MIMIR_SPLIT_AUTO) {
+    if (a.split_flag != nullptr) {
+      work = flag(a.split_flag) != 0;
+    } else {
+      const int lane = threadIdx.x & 63;
+      int any = 0;
+#pragma unroll
+      for (int i = 0; i < kKScanSlots / 64; ++i) any |= flag(&a.kscan[i * 64 + lane]);
+      work = __builtin_amdgcn_ballot_w64(any != 0) != 0;
+    }
+  }
+  if (!work) return;
+  dq_tiles<128>(a, blockIdx.x);
+}
+
+template <int D, bool kCompanion = false>
 hipError_t launch(BwdArgs a, int numseqs, int max_seqlen_all, hipStream_t stream) {
   static_assert(kBlockQ == kPlanTile, "work-list tiles are the dQ query tiles");
   if (numseqs <= 0 || a.cap_q == 0) return hipSuccess;
   // workgroup r * Hq + h: list entry r, head h
-  hipLaunchKernelGGL(dq_kernel<D>, dim3((unsigned)a.cap_q * (unsigned)a.Hq), dim3(kThreads), 0, stream, a);
+  static_assert(!kCompanion || D == 128, "the companion serves the head_dim 128 hand-off");
+  hipLaunchKernelGGL(kCompanion ? dq_companion_kernel : dq_kernel<D>, dim3((unsigned)a.cap_q * (unsigned)a.Hq),
+                     dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -234,9 +266,7 @@ hipError_t launch_bwd_dq_bf16(const BwdArgs& a, int head_dim, int numseqs, int m
     // or a tile that did not fit the region); otherwise its workgroups exit at once.
     hipError_t e = launch_bwd_dq_ds_bf16(a, numseqs, stream);
     if (e != hipSuccess) return e;
-    BwdArgs c = a;
-    c.dq_companion = 1;
-    return launch<128>(c, numseqs, max_seqlen_all, stream);
+    return launch<128, true>(a, numseqs, max_seqlen_all, stream);
   }
   switch (head_dim) {
     case 64: return launch<64>(a, numseqs, max_seqlen_all, stream);
