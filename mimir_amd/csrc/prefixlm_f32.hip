@@ -83,7 +83,11 @@ __device__ __forceinline__ float dot_tile(const float (&x)[D / 4], const float* 
 // The forward gives each row eight lanes (D / 8 values each; the dot products
 // combine with three cross-lane adds), so 32 rows per workgroup: twice the
 // workgroups, and waves, of four lanes per row on the same batch, which the
-// tile loop's LDS broadcast reads need to hide their latency.
+// tile loop's LDS broadcast reads need to hide their latency.  K / V tiles are
+// double-buffered: each thread loads its share of the next tile into registers
+// before the current tile's arithmetic and stores it to the other LDS buffer
+// after, so one barrier per tile remains and the global loads' latency hides
+// behind the arithmetic (staged synchronously, it was paid once per tile).
 constexpr int kFwdLanes = 8;
 constexpr int kFwdRows = kThreads / kFwdLanes;
 
@@ -91,8 +95,11 @@ template <int D>
 __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
   constexpr int EPL = D / kFwdLanes;
   static_assert(EPL % 4 == 0, "whole float4 per lane");
-  __shared__ __attribute__((aligned(16))) float sK[kTile * D];
-  __shared__ __attribute__((aligned(16))) float sV[kTile * D];
+  constexpr int V4 = D / 4;
+  constexpr int kVecs = kTile * V4 / kThreads;  // float4 of K (and of V) per thread per tile
+  static_assert(kVecs * kThreads == kTile * V4, "a tile divides evenly over the threads");
+  __shared__ __attribute__((aligned(16))) float sK[2][kTile * D];
+  __shared__ __attribute__((aligned(16))) float sV[2][kTile * D];
   const int h = blockIdx.x % a.Hq;
   const int s = blockIdx.x / a.Hq;
   const int tile = a.num_tiles - 1 - (int)blockIdx.y;
@@ -121,11 +128,27 @@ __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
   const float* kb = a.k + (int64_t)g.start * a.k_st + (int64_t)hk * a.k_sh;
   const float* vb = a.v + (int64_t)g.start * a.v_st + (int64_t)hk * a.v_sh;
 
-  for (int k0 = 0; k0 < wg_kend; k0 += kTile) {
-    __syncthreads();
-    stage<D>(sK, kb, a.k_st, k0, g.n);
-    stage<D>(sV, vb, a.v_st, k0, g.n);
-    __syncthreads();
+  // this thread's share of a tile: float4 column c of row `row`, kVecs of them
+  f32x4 nk[kVecs], nv[kVecs];
+  auto fetch = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kVecs; ++i) {
+      const int idx = (int)threadIdx.x + i * kThreads, row = idx / V4, c = idx % V4;
+      const bool in = k0 + row < g.n;
+      nk[i] = in ? *(const f32x4*)&kb[(int64_t)(k0 + row) * a.k_st + 4 * c] : f32x4{0.f, 0.f, 0.f, 0.f};
+      nv[i] = in ? *(const f32x4*)&vb[(int64_t)(k0 + row) * a.v_st + 4 * c] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto put = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kVecs; ++i) {
+      const int idx = (int)threadIdx.x + i * kThreads, row = idx / V4, c = idx % V4;
+      *(f32x4*)&sK[buf][row * D + 4 * c] = nk[i];
+      *(f32x4*)&sV[buf][row * D + 4 * c] = nv[i];
+    }
+  };
+  // The tile's arithmetic; false: no allowed key yet (only for rows with kend <= k0).
+  auto tile_step = [&](int k0, const float* tK, const float* tV) __attribute__((always_inline)) {
     float sc[kTile];
     float mx = -INFINITY;
 #pragma unroll
@@ -133,7 +156,7 @@ __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
       float x = 0.f;
 #pragma unroll
       for (int e = 0; e < EPL; e += 4) {
-        const f32x4 t = *(const f32x4*)&sK[j * D + sub * EPL + e];
+        const f32x4 t = *(const f32x4*)&tK[j * D + sub * EPL + e];
         x = __builtin_fmaf(qv[e], t[0], x);
         x = __builtin_fmaf(qv[e + 1], t[1], x);
         x = __builtin_fmaf(qv[e + 2], t[2], x);
@@ -147,7 +170,7 @@ __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
       mx = fmaxf(mx, x);
     }
     const float m_new = fmaxf(m_run, mx);
-    if (m_new == -INFINITY) continue;  // no allowed key yet (only for rows with kend <= k0)
+    if (m_new == -INFINITY) return;
     const float alpha = fast_exp2((m_run - m_new) * a.scale_log2);
     const float mb = m_new * a.scale_log2;
     l_run *= alpha;
@@ -159,7 +182,7 @@ __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
       l_run += pr;
 #pragma unroll
       for (int e = 0; e < EPL; e += 4) {
-        const f32x4 t = *(const f32x4*)&sV[j * D + sub * EPL + e];
+        const f32x4 t = *(const f32x4*)&tV[j * D + sub * EPL + e];
         acc[e] = __builtin_fmaf(pr, t[0], acc[e]);
         acc[e + 1] = __builtin_fmaf(pr, t[1], acc[e + 1]);
         acc[e + 2] = __builtin_fmaf(pr, t[2], acc[e + 2]);
@@ -167,6 +190,21 @@ __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
       }
     }
     m_run = m_new;
+  };
+
+  if (wg_kend > 0) {
+    fetch(0);
+    put(0);
+  }
+  __syncthreads();
+  for (int k0 = 0, buf = 0; k0 < wg_kend; k0 += kTile, buf ^= 1) {
+    const bool more = k0 + kTile < wg_kend;
+    if (more) fetch(k0 + kTile);  // in flight during this tile's arithmetic
+    tile_step(k0, sK[buf], sV[buf]);
+    // The other buffer's last readers finished this tile's predecessor before the
+    // barrier that ended it; this tile's readers finish before the next barrier.
+    if (more) put(buf ^ 1);
+    __syncthreads();
   }
   if (!valid) return;
   const float inv = 1.f / l_run;
