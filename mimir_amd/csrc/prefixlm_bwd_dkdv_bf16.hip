@@ -77,11 +77,11 @@ __device__ __forceinline__ void dkdv_body(const BwdArgs& a) {
   const int hi = lane >> 5;
   const int rank = blockIdx.x / a.Hkv;
   const int hk = blockIdx.x - rank * a.Hkv;
-  const int4 item = a.plan_k[rank];  // never split for this kernel: part 0
+  const int4 item = load_entry(a.plan_k, rank);  // never split for this kernel: part 0
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int ktile = item.y;
-  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const SeqGeom g = load_seq<true>(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int kb0 = ktile * kDkKeys;
   if (kb0 >= g.n) return;
 

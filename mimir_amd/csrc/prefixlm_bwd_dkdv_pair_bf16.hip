@@ -103,7 +103,7 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a, uint64_t seg) {
   auto run_unit = [&](const int4 item, const int hk, int& nxt) {
   const int s = item.x;
   const int half = item.z;  // 0: the whole tile; 1 / 2: first / second half of its steps
-  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const SeqGeom g = load_seq<true>(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int kb0 = item.y * kPairKeys;
   if (kb0 >= g.n) {  // the work list holds no such tile
     if (tid == 0) nxt = fetch_unit();
@@ -512,7 +512,7 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a, uint64_t seg) {
   int unit = blockIdx.x;
   for (;;) {
     const int rank = unit / a.Hkv;
-    const int4 item = a.plan_k[rank];
+    const int4 item = load_entry(a.plan_k, rank);
     if (item.x < 0) break;  // list padding: the rest of the list is padding too
     int nxt = n_units;
     run_unit(item, unit - rank * a.Hkv, nxt);

@@ -35,12 +35,12 @@ __device__ __forceinline__ void dq_tiles(const BwdArgs& a, int b) {
   const int hi = lane >> 5;
   const int rank = b / a.Hq;
   const int h = b - rank * a.Hq;
-  const int4 item = a.plan[rank];
+  const int4 item = load_entry(a.plan, rank);
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int qtile = item.y;
   const int part = item.z & 0xffff, parts = item.z >> 16;
-  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const SeqGeom g = load_seq<true>(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = qtile * kBlockQ;
   if (m0 >= g.nq) return;
   const int hk = h / a.group;

@@ -66,19 +66,53 @@ constexpr int kXcds = 8;
 
 // Sequence bounds are clamped to the packed length T so that malformed metadata
 // can never address memory outside the [T, ...] tensors.
+// Loads through the constant address space: with a wave-uniform index they
+// are scalar loads (the constant cache, one instruction per wave, into scalar
+// registers), otherwise ordinary vector loads.  Only for memory no kernel
+// running beside the reader writes: the work lists (the prologue's, finished
+// before the consumer starts) and the sequence metadata.
+template <typename T>
+__device__ __forceinline__ T load_const(const T* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) T*)p)[i];
+}
+// A work-list entry, whole, for a whole workgroup (i uniform): one scalar load
+// waited for at once (the compiler would otherwise load the first word alone
+// for the padding test and the rest behind it).
+__device__ __forceinline__ int4 load_entry(const int4* list, int i) {
+  const int* w = (const int*)list + 4 * (int64_t)i;
+  const int x = load_const(w, 0), y = load_const(w, 1), z = load_const(w, 2), v = load_const(w, 3);
+  __asm__ volatile("" ::"s"(x), "s"(y), "s"(z), "s"(v));
+  return make_int4(x, y, z, v);
+}
+
+// kUniform: s is the same for the whole workgroup; the three loads are then
+// scalar loads waited for together, before any branch the compiler could sink
+// one of them behind (which costs a kernel another round trip to memory before
+// its first tile).
+template <bool kUniform = false>
 __device__ __forceinline__ SeqGeom load_seq(const int32_t* __restrict__ cu_seqlens,
                                             const int32_t* __restrict__ prefix_lens, int s,
                                             int total_seqlen, int is_causal, int T) {
   SeqGeom g;
-  int start = cu_seqlens[s];
-  int end = cu_seqlens[s + 1];
+  int start, end, p;
+  if constexpr (kUniform) {
+    // the prefix length is read whether or not it is used, and masked
+    start = load_const(cu_seqlens, s);
+    end = load_const(cu_seqlens, s + 1);
+    const int pl = load_const(prefix_lens, s);
+    __asm__ volatile("" ::"s"(start), "s"(end), "s"(pl));
+    p = pl & (is_causal ? 0 : -1);
+  } else {
+    start = cu_seqlens[s];
+    end = cu_seqlens[s + 1];
+    p = is_causal ? 0 : prefix_lens[s];
+  }
   start = start < 0 ? 0 : (start > T ? T : start);
   end = end < start ? start : (end > T ? T : end);
   g.start = start;
   g.n = end - start;
   int nq = total_seqlen - g.start;
   g.nq = nq < 0 ? 0 : (nq > g.n ? g.n : nq);
-  int p = is_causal ? 0 : prefix_lens[s];
   g.p = p < 0 ? 0 : (p > g.n ? g.n : p);
   return g;
 }

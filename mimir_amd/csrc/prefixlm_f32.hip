@@ -103,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void fwd_f32_kernel(const F32Args a) {
   const int h = blockIdx.x % a.Hq;
   const int s = blockIdx.x / a.Hq;
   const int tile = a.num_tiles - 1 - (int)blockIdx.y;
-  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const SeqGeom g = load_seq<true>(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = tile * kFwdRows;
   if (m0 >= g.nq) return;
   const int hk = h / a.group;
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(kThreads) void dq_f32_kernel(const F32Args a) {
   const int h = blockIdx.x % a.Hq;
   const int s = blockIdx.x / a.Hq;
   const int tile = a.num_tiles - 1 - (int)blockIdx.y;
-  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const SeqGeom g = load_seq<true>(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = tile * kRowsPerBlock;
   if (m0 >= g.nq) return;
   const int hk = h / a.group;
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void dkdv_f32_kernel(const F32Args a) {
   const int hk = blockIdx.x % a.Hkv;
   const int s = blockIdx.x / a.Hkv;
   const int tile = blockIdx.y;
-  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const SeqGeom g = load_seq<true>(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int k0 = tile * kRowsPerBlock;
   if (k0 >= g.n) return;
   const int sub = threadIdx.x & 3;

@@ -121,12 +121,12 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, uint64_t seg) {
   if (unit >= a.cap * hkv) return;
   const int rank = unit / hkv;
   const int h = (unit - rank * hkv) * a.group + slot % a.group;
-  const int4 item = a.plan[rank];
+  const int4 item = load_entry(a.plan, rank);
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int mtile = item.y;
   const int part = item.z & 0xffff, parts = item.z >> 16;
-  const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
+  const SeqGeom g = load_seq<true>(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = mtile * kBlockM;
   if (m0 >= g.nq) return;
   const int hk = h / a.group;
