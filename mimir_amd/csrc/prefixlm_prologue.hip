@@ -257,7 +257,13 @@ __device__ int bucket_starts(PlanSmem& sm, double threshold, int max_pairs) {
     run += cnt[j];     // items of cost >= b
     if (max_pairs > 0 && (double)b > threshold && run <= max_pairs) cut = b;
   }
-  if (max_pairs > 0 && cut != 0x7fffffff) atomicMin(&sm.cut, cut);
+  if (max_pairs > 0) {  // uniform
+    // the wave's minimum first, then one LDS atomic per wave: every thread's
+    // atomic on the one word serialized to ~2.5 us
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cut = min(cut, __shfl_xor(cut, off, 64));
+    if ((threadIdx.x & 63) == 0 && cut != 0x7fffffff) atomicMin(&sm.cut, cut);
+  }
   __syncthreads();
   return total;
 }
