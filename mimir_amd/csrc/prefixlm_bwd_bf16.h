@@ -31,7 +31,7 @@ struct BwdArgs {
   int group;
   int total_seqlen;
   int is_causal;
-  int4* plan_q;      // workspace: query-tile work list (sequence, tile, part | parts << 16, chunk slot), for dQ
+  int4* plan_q;      // workspace: query-tile work list (sequence, tile, part | parts << 8 | span << 16, chunk slot), for dQ
   int4* plan_k;      // workspace: key-tile work list (read by the dK / dV stage)
   int cap_q, cap_k;  // entries of each list
   const int4* plan;  // the query-tile list, for the dQ kernel
@@ -77,7 +77,7 @@ __device__ __forceinline__ bool dq_merge_parts(const BwdArgs& a, uint64_t seg, i
                                                f32x16 (&acc)[DT]) {
   __shared__ int later;
   constexpr int kDevScope = 16;  // buffer cache policy: coherent at device scope
-  const int part = item.z & 0xffff, parts = item.z >> 16;
+  const int part = item.z & 0xff, parts = (item.z >> 8) & 0xff;
   const int slot0 = item.w - part;
   const uint32_t slot_bytes = (uint32_t)chunk_slot_bytes(DT * 32);
   char* const base = kernarg_at<char*>(seg, offsetof(BwdArgs, chunk_part));

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int qtile = item.y;
-  const int part = item.z & 0xffff, parts = item.z >> 16;
+  const int part = item.z & 0xff, parts = (item.z >> 8) & 0xff, span = item.z >> 16;
   const SeqGeom g = load_seq(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = qtile * kBlockQ;
   if (m0 >= g.nq) return;
@@ -64,9 +64,10 @@ __global__ __launch_bounds__(kThreads, 2) void dq_ds_kernel(const BwdArgs a) {
 
   const int wg_kend = max(g.p, min(m0 + kBlockQ, g.nq));
   const int nkt_all = (wg_kend + kBlockK - 1) / kBlockK;
-  // key tiles [kt0, nkt) of this part (the whole range unless the list cut it)
-  const int kt0 = (int)((int64_t)part * nkt_all / parts);
-  const int nkt = (int)((int64_t)(part + 1) * nkt_all / parts);
+  // key tiles [kt0, nkt) of this part: the whole range unless the list cut it, then
+  // the last parts `span` tiles each and the first the rest
+  const int kt0 = part == 0 ? 0 : nkt_all - (parts - part) * span;
+  const int nkt = nkt_all - (parts - 1 - part) * span;
   const int qa = m0 + wave * 32;
   const bool wave_active = qa < g.nq;
   const int w_kend_max = wave_active ? max(g.p, min(qa + 32, g.nq)) : 0;

@@ -490,11 +490,12 @@ struct PlanArgs {
   const int32_t* prefix_lens;
   int numseqs, total_seqlen, is_causal, T, kind, group, cap;
   void* items;     // int2 [cap] (kind 0) or int4 [cap] (kinds 1 and 2)
-  // kind 2 (the forward's query tiles, int4 (sequence, tile, part | parts << 16,
-  // chunk slot)): when the grid is small (items * split_heads < slots) the key
-  // range of every item costing more than (total cost * split_heads / slots,
-  // at least kChunkMinCost) is cut into parts of about that cost, at most
-  // kChunkMax; max_pairs (the chunk slots available) = 0 disables it.
+  // kind 2 (the forward's query tiles, int4 (sequence, tile, part | parts << 8 |
+  // span << 16, chunk slot)): when the grid is small (items * split_heads <
+  // slots) the key range of every item costing more than span = ceil(total cost
+  // * split_heads / slots) key tiles (at least kChunkMinCost) is cut into parts,
+  // at most kChunkMax: the last parts span tiles each, the first the rest;
+  // max_pairs (the chunk slots available) = 0 disables it.
   // kind 1: split items costing more than (total cost * split_heads / slots) / 2,
   // heaviest first and whole cost buckets at a time, up to max_pairs items;
   // split_heads = 0 disables splitting.

@@ -44,7 +44,7 @@ struct FwdArgs {
   int group;         // Hq / Hkv
   int total_seqlen;
   int is_causal;
-  const int4* plan;  // (sequence, query tile, part | parts << 16, chunk slot), heaviest first (prefixlm_prologue.hip)
+  const int4* plan;  // (sequence, query tile, part | parts << 8 | span << 16, chunk slot), heaviest first (prefixlm_prologue.hip)
   int cap;           // entries of the list
   float scale;       // softmax scale
   float scale_log2;  // softmax scale * log2(e)
@@ -125,7 +125,7 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, uint64_t seg) {
   if (item.x < 0) return;  // list padding
   const int s = item.x;
   const int mtile = item.y;
-  const int part = item.z & 0xffff, parts = item.z >> 16;
+  const int part = item.z & 0xff, parts = (item.z >> 8) & 0xff, span = item.z >> 16;
   const SeqGeom g = load_seq<true>(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int m0 = mtile * kBlockM;
   if (m0 >= g.nq) return;
@@ -134,9 +134,10 @@ __device__ __forceinline__ void fwd_body(const FwdArgs& a, uint64_t seg) {
   const int wg_qend = min(m0 + kBlockM, g.nq);
   const int wg_kend = max(g.p, wg_qend);
   const int nkt_all = (wg_kend + kBlockN - 1) / kBlockN;
-  // key tiles [kt0, kt1) of this part (the whole range unless the list cut it)
-  const int kt0 = (int)((int64_t)part * nkt_all / parts);
-  const int nkt = (int)((int64_t)(part + 1) * nkt_all / parts);
+  // key tiles [kt0, nkt) of this part: the whole range unless the list cut it, then
+  // the last parts `span` tiles each and the first the rest
+  const int kt0 = part == 0 ? 0 : nkt_all - (parts - part) * span;
+  const int nkt = nkt_all - (parts - 1 - part) * span;
 
   const int qa = m0 + wave * 32;
   const bool wave_active = qa < g.nq;

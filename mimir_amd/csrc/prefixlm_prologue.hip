@@ -132,11 +132,13 @@ __device__ __forceinline__ int wave_alloc(int* counter, int n) {
   return base + x - n;
 }
 
-// Parts of a kind-2 item of cost c at part cost `target` (0: no chunking).
-__device__ __forceinline__ int chunk_parts(int c, double target) {
-  if (target <= 0.0 || (double)c <= target) return 1;
-  const double n = ceil((double)c / target);
-  return n < (double)kChunkMax ? (int)n : kChunkMax;
+// Parts of a kind-2 item of cost c cut at `span` key tiles per part (0: no
+// chunking): the last parts run `span` tiles each, the first the rest, so that
+// the cut leaves whole-slot parts and one remainder for the end of the list.
+__device__ __forceinline__ int chunk_parts(int c, int span) {
+  if (span <= 0 || c <= span) return 1;
+  const int n = (c + span - 1) / span;
+  return n < kChunkMax ? n : kChunkMax;
 }
 
 // Visits every (sequence, tile) item, 256 sequences at a time: a scan of the
@@ -144,14 +146,14 @@ __device__ __forceinline__ int chunk_parts(int c, double target) {
 // the threads one each, so a single long sequence is spread over the workgroup
 // too.  Items costing `cut` or more count as two halves.  Without kScatter the
 // visit adds each item (or half) to its cost bucket; with kScatter it takes the
-// next position of that bucket and writes the entry.  Kind 2 with `target` > 0
-// cuts items into chunk_parts(cost, target) parts instead.  With `reuse` (only
+// next position of that bucket and writes the entry.  Kind 2 with `span` > 0
+// cuts items into chunk_parts(cost, span) parts instead.  With `reuse` (only
 // for numseqs <= kThreads, after a walk of the same list) the sequences' first
 // items and geometry are still in `sm` and are not loaded again; `pre` is this
 // thread's sequence of the first chunk, loaded by the caller ahead of time.
 // Returns this thread's share of the total cost.
 template <bool kScatter>
-__device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut, double target = 0.0, bool reuse = false,
+__device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut, int span = 0, bool reuse = false,
                              const SeqGeom* pre = nullptr, int* items = nullptr) {
   double cost_sum = 0.0;
   if (items != nullptr) *items = 0;
@@ -193,24 +195,31 @@ __device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut, double ta
         c = item_cost(sm.p[j], sm.nq[j], a.kind, a.group, t);
         cost_sum += (double)c;
       }
-      const int parts = valid && a.kind == 2 ? chunk_parts(c, target) : 1;
+      const int parts = valid && a.kind == 2 ? chunk_parts(c, span) : 1;
       int slot = 0;  // first chunk slot (kind 2 parts) or pair index (kind 1 halves)
-      if (kScatter && (a.kind == 2 ? target > 0.0 : cut != 0x7fffffff)) {  // uniform
-        const int n = !valid ? 0 : a.kind == 2 ? (parts > 1 ? parts : 0) : (a.kind == 1 && c >= cut ? 1 : 0);
-        slot = wave_alloc(&sm.pairs, n);
+      int spos = 0;  // kind 2: position (scatter) of the item's span-tile parts 1 ..
+      if (a.kind == 2 && span > 0) {  // uniform
+        const int n = valid && parts > 1 ? parts : 0;
+        if (kScatter) slot = wave_alloc(&sm.pairs, n);
+        // the span-tile parts of every cut item share one bucket: one LDS atomic
+        // per wave (per-lane atomics on one word serialize)
+        spos = wave_alloc(&sm.hist[hist_slot(span)], n > 0 ? n - 1 : 0);
+      } else if (kScatter && a.kind != 2 && cut != 0x7fffffff) {  // uniform
+        slot = wave_alloc(&sm.pairs, valid && a.kind == 1 && c >= cut ? 1 : 0);
       }
       if (!valid) continue;
       if (parts > 1) {
-        const int cp = (c + parts - 1) / parts;
-        if constexpr (kScatter) {  // the parts take consecutive positions and slots
-          const int pos = atomicAdd(&sm.hist[hist_slot(cp)], parts);
-          for (int q = 0; q < parts; ++q) put_item(a, pos + q, base + j, t, q | (parts << 16), slot + q);
+        const int c0 = c - (parts - 1) * span;  // the first part's tiles, the others `span`
+        const int z = (parts << 8) | (span << 16);
+        if constexpr (kScatter) {  // parts 1.. take consecutive positions; every part its slot
+          put_item(a, atomicAdd(&sm.hist[hist_slot(c0)], 1), base + j, t, z, slot);
+          for (int q = 1; q < parts; ++q) put_item(a, spos + q - 1, base + j, t, q | z, slot + q);
         } else {
-          atomicAdd(&sm.hist[hist_slot(cp)], parts);
+          atomicAdd(&sm.hist[hist_slot(c0)], 1);
         }
       } else if (a.kind == 2) {
         if constexpr (kScatter) {
-          put_item(a, atomicAdd(&sm.hist[hist_slot(c)], 1), base + j, t, 1 << 16, -1);
+          put_item(a, atomicAdd(&sm.hist[hist_slot(c)], 1), base + j, t, 1 << 8, -1);
         } else {
           atomicAdd(&sm.hist[hist_slot(c)], 1);
         }
@@ -281,11 +290,12 @@ __device__ double block_sum(double v, PlanSmem& sm) {
 
 // A query-tile list (kind 2: the forward's, dQ's): counted once (items and
 // cost); if the grid is small (fewer workgroups than a.slots resident at once)
-// the items costing more than the per-workgroup average of one round are cut
-// into parts (chunk_parts) and the counts are redone with the parts; then the
-// bucket positions are scanned and the list is written.  The parts of all
-// items number at most 2 * a.slots / a.split_heads <= a.max_pairs (each part
-// of a cut item costs more than half the target), so the chunk slots suffice.
+// the items costing more than the per-workgroup average of one round (the
+// span, in whole key tiles) are cut into parts (chunk_parts) and the counts are
+// redone with the parts; then the bucket positions are scanned and the list is
+// written.  A cut item of cost c > span has ceil(c / span) < 2 c / span parts,
+// so the parts of all items number fewer than 2 * a.slots / a.split_heads <=
+// a.max_pairs: the chunk slots suffice.
 // The first chunk's sequence geometry, loaded before the zeroing so that its
 // latency overlaps it.
 __device__ __forceinline__ SeqGeom prefetch_seq(const PlanArgs& a) {
@@ -305,17 +315,17 @@ __device__ void plan_block_chunks(const PlanArgs& a, PlanSmem& sm) {
   const double mine = walk_items<false>(a, sm, 0x7fffffff, 0.0, false, &pre, &items);
   const bool reuse = a.numseqs <= kThreads;  // one chunk of sequences: still in sm
   int total;
-  double target = 0.0;
+  int span = 0;
   if (a.max_pairs > 0 && a.split_heads > 0 && (int64_t)items * a.split_heads < (int64_t)a.slots) {
     // small grid: recount with the cut items' parts (the first counts are not used)
-    target = block_sum(mine, sm) * a.split_heads / a.slots;
-    if (target < (double)kChunkMinCost) target = (double)kChunkMinCost;
+    const double target = block_sum(mine, sm) * a.split_heads / a.slots;
+    span = target > (double)kChunkMinCost ? (int)ceil(target) : kChunkMinCost;
     for (int i = threadIdx.x; i < kHistSlots; i += kThreads) sm.hist[i] = 0;
     __syncthreads();
-    walk_items<false>(a, sm, 0x7fffffff, target, reuse);
+    walk_items<false>(a, sm, 0x7fffffff, span, reuse);
   }
   total = bucket_starts(sm, 0.0, 0);
-  walk_items<true>(a, sm, 0x7fffffff, target, reuse);
+  walk_items<true>(a, sm, 0x7fffffff, span, reuse);
   for (int i = total + threadIdx.x; i < a.cap; i += kThreads) put_item(a, i, -1, -1, 0, -1);
 }
 

@@ -54,10 +54,11 @@ def key_chunks():
 def check_plan(case, lst, hq, chunked):
     """The query-tile list pinned against its definition: every 128-row tile of every sequence
     appears exactly once, whole (part 0 of 1, no chunk slot) or as parts 0 .. parts - 1 with
-    consecutive chunk slots no other tile uses; a tile is cut, into ceil(cost / target) parts (at
-    most 16), exactly when the grid is small (tiles x Hq < 512) and its cost exceeds target =
-    max(total cost x Hq / 512, 4) (cost: the key tiles of 64 its rows attend); entries run heaviest
-    first by the cost of what each runs, ceil(cost / parts); padding (-1) only after the last."""
+    consecutive chunk slots no other tile uses; a tile is cut exactly when the grid is small
+    (tiles x Hq < 512) and its cost exceeds span = ceil(max(total cost x Hq / 512, 4)) (cost: the
+    key tiles of 64 its rows attend), into ceil(cost / span) parts (at most 16) whose key ranges the
+    kernels take as: the last parts span tiles each, part 0 the rest; entries run heaviest first
+    by the cost of what each runs; padding (-1) only after the last."""
     total = int(case.total_seqlen)
     cu = [int(x) for x in case.cu_seqlens[: len(case.seq_lens) + 1]]
     expect = {}
@@ -68,29 +69,36 @@ def check_plan(case, lst, hq, chunked):
             expect[(s, t)] = -(-max(p, min(128 * t + 128, nq)) // 64)
     cost_total = sum(expect.values())
     small = chunked and len(expect) * hq < 512
-    target = max(cost_total * hq / 512, 4.0) if small else 0.0
+    span = math.ceil(max(cost_total * hq / 512, 4.0)) if small else 0
     seen, costs, slots, padding = {}, [], set(), False
     for x, y, z, w in lst.tolist():
         if x < 0:
             padding = True
             continue
         assert not padding, "an entry after the padding"
-        part, parts = z & 0xFFFF, z >> 16
+        part, parts, zspan = z & 0xFF, (z >> 8) & 0xFF, z >> 16
         c = expect[(x, y)]
-        want = 1 if not small or c <= target else min(math.ceil(c / target), 16)
+        want = 1 if not small or c <= span else min(math.ceil(c / span), 16)
         assert parts == want, ((x, y), c, parts, want)
         if parts == 1:
-            assert part == 0 and w == -1
+            assert part == 0 and w == -1 and zspan == 0
+            runs = c
         else:
-            assert 0 <= part < parts and w >= 0 and w not in slots
+            assert 0 <= part < parts and w >= 0 and w not in slots and zspan == span
             slots.add(w)
-        seen.setdefault((x, y), []).append((part, w))
-        costs.append(min(-(-c // parts), 4095))
+            # the kernels' key range of this part: [kt0, kt1) of the tile's c key tiles
+            kt0 = 0 if part == 0 else c - (parts - part) * span
+            kt1 = c - (parts - 1 - part) * span
+            assert 0 <= kt0 < kt1 <= c
+            runs = kt1 - kt0
+        seen.setdefault((x, y), []).append((part, w, runs))
+        costs.append(min(runs, 4095))
     assert set(seen) == set(expect)
     for key, ps in seen.items():
         ps.sort()
-        assert [q for q, _ in ps] == list(range(len(ps)))
-        assert len({w - q for q, w in ps}) == 1  # consecutive slots
+        assert [q for q, _, _ in ps] == list(range(len(ps)))
+        assert len({w - q for q, w, _ in ps}) == 1  # consecutive slots
+        assert sum(r for _, _, r in ps) == expect[key]  # the parts cover the key range once
     assert all(a >= b for a, b in zip(costs, costs[1:])), "not heaviest first"
 
 
@@ -109,7 +117,7 @@ def forward(c, chunks, case=None, **kw):
     if p.workspace_bytes > lib.mimir_prefixlm_fwd_workspace_bytes(c.T, int(c.numseqs), int(c.max_seqlen_all)):
         entries += 1024 // c.q.shape[1]  # the chunk slots' list entries
     lst = ws.view(torch.int32)[: 4 * entries].view(-1, 4).cpu()
-    cut = int(((lst[:, 0] >= 0) & ((lst[:, 2] >> 16) > 1)).sum())
+    cut = int(((lst[:, 0] >= 0) & (((lst[:, 2] >> 8) & 0xFF) > 1)).sum())
     if case is not None:
         check_plan(case, lst, c.q.shape[1], chunks)
     res = {"o": out.clone(), "lse": lse.clone()}
@@ -255,7 +263,7 @@ def backward(c, out, lse, chunks, d, case=None):
             entries = -(-c.T // 128) + int(c.numseqs) + 1024 // c.q.shape[1]
             ws = keep[9].view(torch.uint8)[_align(base): _align(base) + 16 * entries].view(torch.int32)
             lst = ws.view(-1, 4).cpu()
-            cut = int(((lst[:, 0] >= 0) & ((lst[:, 2] >> 16) > 1)).sum())
+            cut = int(((lst[:, 0] >= 0) & (((lst[:, 2] >> 8) & 0xFF) > 1)).sum())
             if case is not None:
                 check_plan(case, lst, c.q.shape[1], True)
     return dq.clone(), dk.clone(), dv.clone(), cut
