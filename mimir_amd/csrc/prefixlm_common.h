@@ -500,6 +500,9 @@ struct PlanArgs {
   // heaviest first and whole cost buckets at a time, up to max_pairs items;
   // split_heads = 0 disables splitting.
   int split_heads, max_pairs, slots;
+  // kind 2: the part span in percent of the per-slot average (>= 100, so that the
+  // parts stay within max_pairs)
+  int span_pct;
   int* zero;  // n_zero int32 set to 0 (the consumer's counters)
   int n_zero;
 };

@@ -318,7 +318,7 @@ __device__ void plan_block_chunks(const PlanArgs& a, PlanSmem& sm) {
   int span = 0;
   if (a.max_pairs > 0 && a.split_heads > 0 && (int64_t)items * a.split_heads < (int64_t)a.slots) {
     // small grid: recount with the cut items' parts (the first counts are not used)
-    const double target = block_sum(mine, sm) * a.split_heads / a.slots;
+    const double target = block_sum(mine, sm) * a.split_heads / a.slots * (a.span_pct < 100 ? 100 : a.span_pct) / 100.0;
     span = target > (double)kChunkMinCost ? (int)ceil(target) : kChunkMinCost;
     for (int i = threadIdx.x; i < kHistSlots; i += kThreads) sm.hist[i] = 0;
     __syncthreads();
@@ -589,6 +589,7 @@ PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int nu
   a.split_heads = 0;
   a.max_pairs = 0;
   a.slots = 0;
+  a.span_pct = 100;
   a.zero = nullptr;
   a.n_zero = 0;
   return a;

@@ -51,11 +51,12 @@ def key_chunks():
     P._key_chunks = saved
 
 
-def check_plan(case, lst, hq, chunked):
+def check_plan(case, lst, hq, chunked, span_pct):
     """The query-tile list pinned against its definition: every 128-row tile of every sequence
     appears exactly once, whole (part 0 of 1, no chunk slot) or as parts 0 .. parts - 1 with
     consecutive chunk slots no other tile uses; a tile is cut exactly when the grid is small
-    (tiles x Hq < 512) and its cost exceeds span = ceil(max(total cost x Hq / 512, 4)) (cost: the
+    (tiles x Hq < 512) and its cost exceeds span = ceil(max(total cost x Hq / 512 x span_pct / 100,
+    4)) (span_pct 125 for the forward's list, 100 for dQ's; cost: the
     key tiles of 64 its rows attend), into ceil(cost / span) parts (at most 16) whose key ranges the
     kernels take as: the last parts span tiles each, part 0 the rest; entries run heaviest first
     by the cost of what each runs; padding (-1) only after the last."""
@@ -69,7 +70,8 @@ def check_plan(case, lst, hq, chunked):
             expect[(s, t)] = -(-max(p, min(128 * t + 128, nq)) // 64)
     cost_total = sum(expect.values())
     small = chunked and len(expect) * hq < 512
-    span = math.ceil(max(cost_total * hq / 512, 4.0)) if small else 0
+    target = cost_total * hq / 512 * span_pct / 100.0
+    span = (math.ceil(target) if target > 4.0 else 4) if small else 0
     seen, costs, slots, padding = {}, [], set(), False
     for x, y, z, w in lst.tolist():
         if x < 0:
@@ -119,7 +121,7 @@ def forward(c, chunks, case=None, **kw):
     lst = ws.view(torch.int32)[: 4 * entries].view(-1, 4).cpu()
     cut = int(((lst[:, 0] >= 0) & (((lst[:, 2] >> 8) & 0xFF) > 1)).sum())
     if case is not None:
-        check_plan(case, lst, c.q.shape[1], chunks)
+        check_plan(case, lst, c.q.shape[1], chunks, 125)
     res = {"o": out.clone(), "lse": lse.clone()}
     for name, t in kw.items():
         if isinstance(t, torch.Tensor) and t.dtype == c.q.dtype:
@@ -265,7 +267,7 @@ def backward(c, out, lse, chunks, d, case=None):
             lst = ws.view(-1, 4).cpu()
             cut = int(((lst[:, 0] >= 0) & (((lst[:, 2] >> 8) & 0xFF) > 1)).sum())
             if case is not None:
-                check_plan(case, lst, c.q.shape[1], True)
+                check_plan(case, lst, c.q.shape[1], True, 100)
     return dq.clone(), dk.clone(), dv.clone(), cut
 
 
