@@ -118,6 +118,10 @@ hipError_t launch(const MimirPrefixLMBwdParams& p, Prologue pro, hipStream_t str
       pk.split_heads = a.Hkv;
       pk.max_pairs = ws.pair_heads / a.Hkv;
       pk.slots = device_cu_count();
+      // a split item's first half runs the per-CU average of steps, its second the
+      // rest (equal halves left the XXS queue a tail of half-units: dK/dV 0.120 ->
+      // 0.108 ms there, packed documents -1%, 8 x 2048 unchanged)
+      pk.span_pct = 100;
     }
     pk.zero = a.split_ctr;  // split counters, the dK / dV work queue and the dS-incomplete flag
     pk.n_zero = ws.pair_heads + kCounterWordsAfterPairs;

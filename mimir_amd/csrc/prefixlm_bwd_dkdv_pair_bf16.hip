@@ -102,7 +102,8 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a, uint64_t seg) {
   // the queue hands out units in list order to whichever workgroup frees up.
   auto run_unit = [&](const int4 item, const int hk, int& nxt) {
   const int s = item.x;
-  const int half = item.z;  // 0: the whole tile; 1 / 2: first / second half of its steps
+  const int half = item.z & 0xff;  // 0: the whole tile; 1 / 2: its steps before / from the split
+  const int split_at = item.z >> 8;  // the split step (0: the middle)
   const SeqGeom g = load_seq<true>(a.cu_seqlens, a.prefix_lens, s, a.total_seqlen, a.is_causal, a.T);
   const int kb0 = item.y * kPairKeys;
   if (kb0 >= g.n) {  // the work list holds no such tile
@@ -118,8 +119,9 @@ __device__ __forceinline__ void dkdv_pair_body(const BwdArgs& a, uint64_t seg) {
   const int q_begin = qstart_of(g.p, kb0);
   const int nqt = g.nq > q_begin ? (g.nq - q_begin + kBwdBlockQT - 1) / kBwdBlockQT : 0;
   const int n_all = nqt * a.group;
-  const int it_lo = half == 2 ? n_all / 2 : 0;
-  const int n_iter = (half == 1 ? n_all / 2 : n_all) - it_lo;
+  const int s1 = split_at > 0 ? min(split_at, n_all) : n_all / 2;
+  const int it_lo = half == 2 ? s1 : 0;
+  const int n_iter = (half == 1 ? s1 : n_all) - it_lo;
   const int head0 = nqt > 0 ? it_lo / nqt : 0;  // first step: q head hk * G + head0, query tile tile0
   const int tile0 = it_lo - head0 * nqt;
   // dS blocks of this wave: key block ka / 32 of block row floor(start / 32) + s + query / 32.

@@ -501,7 +501,8 @@ struct PlanArgs {
   // split_heads = 0 disables splitting.
   int split_heads, max_pairs, slots;
   // kind 2: the part span in percent of the per-slot average (>= 100, so that the
-  // parts stay within max_pairs)
+  // parts stay within max_pairs); kind 1: a split item's first half in percent of
+  // the per-CU average (0: half its steps)
   int span_pct;
   int* zero;  // n_zero int32 set to 0 (the consumer's counters)
   int n_zero;

@@ -224,10 +224,10 @@ __device__ double walk_items(const PlanArgs& a, PlanSmem& sm, int cut, int span 
           atomicAdd(&sm.hist[hist_slot(c)], 1);
         }
       } else if (c >= cut) {
-        const int c1 = c / 2, c2 = c - c1;
-        if constexpr (kScatter) {
-          put_item(a, atomicAdd(&sm.hist[hist_slot(c1)], 1), base + j, t, 1, slot);
-          put_item(a, atomicAdd(&sm.hist[hist_slot(c2)], 1), base + j, t, 2, slot);
+        const int c1 = span > 0 ? span : c / 2, c2 = c - c1;
+        if constexpr (kScatter) {  // half | first step of half 2 << 8 (0: the middle)
+          put_item(a, atomicAdd(&sm.hist[hist_slot(c1)], 1), base + j, t, 1 | (span << 8), slot);
+          put_item(a, atomicAdd(&sm.hist[hist_slot(c2)], 1), base + j, t, 2 | (span << 8), slot);
         } else {
           atomicAdd(&sm.hist[hist_slot(c1)], 1);
           atomicAdd(&sm.hist[hist_slot(c2)], 1);
@@ -346,17 +346,25 @@ __device__ void plan_block(const PlanArgs& a) {
   __syncthreads();
   const double mine = walk_items<false>(a, sm, 0x7fffffff, 0.0, false, &pre);
   double threshold = 0.0;
-  if (split)  // half the average per compute unit
-    threshold = block_sum(mine, sm) * a.split_heads / a.slots / 2.0;
+  int span = 0;  // the first half's steps of a split item (0: half of them)
+  if (split) {
+    const double avg = block_sum(mine, sm) * a.split_heads / a.slots;  // per compute unit
+    if (a.span_pct > 0) {
+      span = (int)ceil(avg * a.span_pct / 100.0);
+      threshold = span;
+    } else {
+      threshold = avg / 2.0;
+    }
+  }
   int total = bucket_starts(sm, threshold, split ? a.max_pairs : 0);
-  const int cut = sm.cut;
-  if (cut != 0x7fffffff) {  // recount with the heavy items halved
+  const int cut = sm.cut;  // > threshold: a split item's halves are non-empty
+  if (cut != 0x7fffffff) {  // recount with the heavy items split
     for (int i = threadIdx.x; i < kHistSlots; i += kThreads) sm.hist[i] = 0;
     __syncthreads();
-    walk_items<false>(a, sm, cut, 0.0, a.numseqs <= kThreads);
+    walk_items<false>(a, sm, cut, span, a.numseqs <= kThreads);
     total = bucket_starts(sm, 0.0, 0);
   }
-  walk_items<true>(a, sm, cut, 0.0, a.numseqs <= kThreads);
+  walk_items<true>(a, sm, cut, span, a.numseqs <= kThreads);
   for (int i = total + threadIdx.x; i < a.cap; i += kThreads) put_item(a, i, -1, -1, 0, -1);
 }
 
@@ -589,7 +597,7 @@ PlanArgs plan_args(const int32_t* cu_seqlens, const int32_t* prefix_lens, int nu
   a.split_heads = 0;
   a.max_pairs = 0;
   a.slots = 0;
-  a.span_pct = 100;
+  a.span_pct = kind == 2 ? 100 : 0;
   a.zero = nullptr;
   a.n_zero = 0;
   return a;
