@@ -186,7 +186,10 @@ def _geometry(q: Tensor, k: Tensor, v: Tensor):
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The device's current stream, as the raw handle torch's own kernel launches use
+    (building a ``torch.cuda.Stream`` for it took ~20 us of host time per call)."""
+    return torch._C._cuda_getCurrentRawStream(device.index if device.index is not None
+                                               else torch.cuda.current_device())
 
 
 def check_metadata(prefix_lens: Tensor, causal_lens: Tensor, cu_seqlens: Tensor, numseqs,
@@ -511,6 +514,13 @@ def _(dout, q, k, v, out, lse, out_lo, split_flag, is_causal, prefix_lens, causa
             torch.empty_like(v, memory_format=cf))
 
 
+def _direct(q: Tensor) -> bool:
+    """Whether a call may run the ops' bodies directly: eager, with plain tensors (no
+    torch.compile, no tracing or fake-tensor mode, which must see the custom ops)."""
+    return (type(q) is Tensor and not torch.compiler.is_compiling()
+            and torch._C._len_torch_dispatch_stack() == 0)
+
+
 def _cpu_scalar(x) -> Tensor:
     if isinstance(x, Tensor):
         return x if x.device.type == "cpu" else x.cpu()
@@ -518,13 +528,19 @@ def _cpu_scalar(x) -> Tensor:
 
 
 class PrefixLMAttention(torch.autograd.Function):
-    """Autograd function over the two custom ops (flash_attention_prefixlm_v2.py:249-283)."""
+    """Autograd function over the two custom ops (flash_attention_prefixlm_v2.py:249-283).
+
+    Under torch.compile the ops are what the graph records; run eagerly it calls
+    their bodies directly, which skips ~50 us of custom-op dispatch per call (at
+    Mimir2's XXS shape the GPU work of a step is ~0.24 ms, so that host time
+    showed)."""
 
     @staticmethod
     def forward(ctx, q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen, numseqs,
                 max_seqlen_all, softmax_scale):
-        out, lse, out_lo, flag = _prefixlm_fwd_op(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens,
-                                                  total_seqlen, numseqs, max_seqlen_all, softmax_scale)
+        fwd = _fwd_impl if _direct(q) else _prefixlm_fwd_op
+        out, lse, out_lo, flag = fwd(q, k, v, is_causal, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
+                                     numseqs, max_seqlen_all, softmax_scale)
         ctx.save_for_backward(q, k, v, out, lse, out_lo, flag, prefix_lens, causal_lens, cu_seqlens, total_seqlen,
                               numseqs, max_seqlen_all)
         ctx.mark_non_differentiable(lse)
@@ -538,9 +554,9 @@ class PrefixLMAttention(torch.autograd.Function):
          max_seqlen_all) = ctx.saved_tensors
         if dout is None:
             dout = torch.zeros_like(out)
-        dq, dk, dv = _prefixlm_bwd_op(dout, q, k, v, out, lse, out_lo, flag, ctx.is_causal, prefix_lens,
-                                      causal_lens, cu_seqlens, total_seqlen, numseqs, max_seqlen_all,
-                                      ctx.softmax_scale)
+        bwd = _bwd_impl if _direct(q) else _prefixlm_bwd_op
+        dq, dk, dv = bwd(dout, q, k, v, out, lse, out_lo, flag, ctx.is_causal, prefix_lens, causal_lens,
+                         cu_seqlens, total_seqlen, numseqs, max_seqlen_all, ctx.softmax_scale)
         return dq, dk, dv, None, None, None, None, None, None, None, None
 
 
